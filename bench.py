@@ -1,0 +1,225 @@
+"""Benchmark of the ternary x int8 GEMM path on one MI355X.
+
+Default workload (one step): the full linear set of one FastConformer layer at T=338 frames, d_model=1024, every
+GEMM on synthetic resident inputs with its epilogue: FF1 up 1024->4096 (SiLU) and down 4096->1024 (AddScaled 0.5),
+stacked q|k|v 1024->3072, pos 1024->1024 on 2T-1=675 rows, out-proj 1024->1024 (AddScaled 1), conv pointwise1
+1024->2048 and pointwise2 1024->1024 (AddScaled 1), FF2 up/down. Trits P(0)=0.4, P(+-1)=0.3; per-output-channel f16
+scales in [0.01, 0.05]; activations N(0,1) quantized per token (group = K). value = ternary x int8 GEMM TOPS
+(2*M*N*K per GEMM, zeros counted) over the timed steps.
+
+Prints one JSON line. Extra keys: "roofline" for the dominant kernel (HIP-event time per launch on the launch
+stream), "cpu_baseline" (the AVX-512 VNNI restatement on the host cores, bounded sample), "details" (the M=338 and
+M=8192 FFN-up GEMM alone, group = K and 128).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
+
+
+def layer_shapes(t: int):
+    """(name, M, K, N, epilogue kind, alpha) of one layer's linear set (encoder.rs:79-94,138-293,582-630)."""
+    return [
+        ("ff1_up", t, 1024, 4096, 1, 0.0),
+        ("ff1_down", t, 4096, 1024, 2, 0.5),
+        ("qkv", t, 1024, 3072, 0, 0.0),
+        ("pos", 2 * t - 1, 1024, 1024, 0, 0.0),
+        ("o_proj", t, 1024, 1024, 2, 1.0),
+        ("pw1", t, 1024, 2048, 0, 0.0),
+        ("pw2", t, 1024, 1024, 2, 1.0),
+        ("ff2_up", t, 1024, 4096, 1, 0.0),
+        ("ff2_down", t, 4096, 1024, 2, 0.5),
+    ]
+
+
+def algo_bytes(m, k, n, group, int32_out=False):
+    """2-bit weights + f32 weight scales + int8 activations + f32 activation scales (+ gsum) + f32 output."""
+    ng = k // group
+    b = n * k / 4 + n * ng * 4 + m * k + m * ng * 8 + m * n * 4
+    return b + (m * n * 4 if int32_out else 0)
+
+
+class Gemm:
+    """One GEMM with resident synthetic operands."""
+
+    def __init__(self, vx, synth, dev, name, m, k, n, ep, alpha, group, cfg, role):
+        import torch
+
+        self.name, self.m, self.k, self.n, self.group = name, m, k, n, group
+        trits = synth.synth_trits(synth.workload_seed(cfg, role), n, k)
+        s16 = synth.synth_channel_scales_f16(synth.workload_seed(cfg, role + 1), n, k // group)
+        x = synth.synth_normal(synth.workload_seed(cfg, role + 2), m * k).reshape(m, k)
+        self.w = vx.TernaryMatrix.from_packed(synth.pack_rows(trits), s16, n, k, group)
+        self.xa = vx.QuantAct.quantize(torch.from_numpy(x).to(dev), group)
+        self.y = torch.zeros((m, n), dtype=torch.float32, device=dev)
+        self.ep = {0: vx.Epilogue.Store, 1: vx.Epilogue.Silu}.get(ep) or vx.Epilogue.AddScaled(alpha)
+        self.vx = vx
+        self.ops = 2.0 * m * n * k
+        self.bytes = algo_bytes(m, k, n, group)
+        self.host = (trits, s16, x)
+
+    def run(self):
+        self.vx.gemm_ep(self.w, self.xa, self.y, None, self.ep)
+
+
+def time_launches(torch, gemms, reps):
+    """Average HIP-event time per launch of each GEMM, on torch's current stream (the launch stream)."""
+    st = torch.cuda.current_stream()
+    out = {}
+    for g in gemms:
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in ev:
+            a.record(st)
+            g.run()
+            b.record(st)
+        torch.cuda.synchronize()
+        out[g.name] = float(np.mean([a.elapsed_time(b) for a, b in ev])) * 1e-3  # seconds
+    return out
+
+
+def roofline_of(g, sec):
+    t_mfma = g.ops / (PEAK_INT8_TOPS * 1e12)
+    t_hbm = g.bytes / (PEAK_HBM_GBS * 1e9)
+    if t_mfma >= t_hbm:
+        a = g.ops / sec / 1e12
+        return {"bound": "mfma", "achieved": round(a, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                "frac": round(a / PEAK_INT8_TOPS, 4)}
+    a = g.bytes / sec / 1e9
+    return {"bound": "hbm", "achieved": round(a, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(a / PEAK_HBM_GBS, 4)}
+
+
+def cpu_baseline(gemms, budget_s=10.0):
+    """The reference's AVX-512 VNNI kernel (C restatement, oracle/vnni_baseline.c) with gemm_ep's row-block split
+    on the host cores, over the same layer's GEMMs, repeated until about `budget_s` of CPU work."""
+    from oracle import oracle
+
+    if not oracle.lib().or_have_vnni():
+        return None
+    threads = min(os.cpu_count() or 1, 16)
+    prepared = []
+    for g in gemms:
+        trits, s16, x = g.host
+        ws = oracle.f16_to_f32(s16)
+        q, xs, gsum = oracle.quantize(x, g.group)
+        wq, sq = oracle.quad16_pack(trits, ws, g.group)
+        y = np.zeros((g.m, g.n), np.float32)
+        prepared.append((g, wq, sq, q, xs, gsum, y))
+
+    def one_pass():
+        for g, wq, sq, q, xs, gsum, y in prepared:
+            oracle.gemm_ep_vnni(wq, sq, g.n, g.k, g.group, q, xs, gsum, y, g.ep.kind, g.ep.alpha, threads=threads)
+
+    one_pass()  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        one_pass()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 1000:
+            break
+    ops = sum(g.ops for g in gemms) * reps
+    return {"value": round(ops / el / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"{reps} passes of the same layer's {len(gemms)} GEMMs (T=338), {el:.1f} s, "
+                      f"{threads} threads, AVX-512 VNNI restatement of kernels/x86.rs with gemm_ep's block split"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-details", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the ternary GEMM path shards by "
+              f"independent clips with no collective, so a multi-GPU figure is N independent copies of this one",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import voxrt_amd as vx
+    from voxrt_amd import synth
+
+    vx.kernels.check(vx.lib().vx_init(0))
+    dev = torch.device("cuda:0")
+    T = 338
+    gemms = [Gemm(vx, synth, dev, name, m, k, n, ep, a, k, 1, 16 * i + 1)
+             for i, (name, m, k, n, ep, a) in enumerate(layer_shapes(T))]
+
+    def step():
+        for g in gemms:
+            g.run()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = e0.elapsed_time(e1) * 1e-3
+    ops = sum(g.ops for g in gemms)
+    value = ops * args.steps / gpu_s / 1e12
+
+    per = time_launches(torch, gemms, 50)
+    dom = max(gemms, key=lambda g: per[g.name])
+    roof = roofline_of(dom, per[dom.name])
+    roof["kernel"] = f"tgemm_kernel ({dom.name}: M={dom.m} K={dom.k} N={dom.n} G={dom.group})"
+    roof["traffic"] = None
+
+    details = {"per_gemm_us": {g.name: round(per[g.name] * 1e6, 2) for g in gemms}}
+    if not args.no_details:
+        extra = []
+        for name, m, k, n, grp in [("ffn_up_t338_gK", 338, 1024, 4096, 1024), ("ffn_up_t338_g128", 338, 1024, 4096, 128),
+                                   ("ffn_up_m8192_gK", 8192, 1024, 4096, 1024),
+                                   ("ffn_up_m8192_g128", 8192, 1024, 4096, 128),
+                                   ("ffn_down_m8192_gK", 8192, 4096, 1024, 4096),
+                                   ("ffn_down_m8192_g128", 8192, 4096, 1024, 128)]:
+            extra.append(Gemm(vx, synth, dev, name, m, k, n, 0, 0.0, grp, 0, 1))
+        for g in extra:
+            for _ in range(5):
+                g.run()
+        pe = time_launches(torch, extra, 30)
+        for g in extra:
+            s = pe[g.name]
+            details[g.name] = {"us": round(s * 1e6, 2), "tops": round(g.ops / s / 1e12, 1),
+                               "pct_int8_peak": round(100 * g.ops / s / 1e12 / PEAK_INT8_TOPS, 1),
+                               "hbm_gbs": round(g.bytes / s / 1e9, 0)}
+        del extra
+    cpu = None if args.no_cpu else cpu_baseline(gemms)
+
+    line = {
+        "metric": "ternary x int8 GEMM TOPS (one FastConformer layer's linear set at T=338)",
+        "value": round(value, 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(gpu_s / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8 x ternary, int32 accumulate, fp32 dequant", "data": "synthetic",
+        "config": {"workload": "layer_linear_set_t338", "T": T, "d_model": 1024, "ffn": 4096, "group": "K",
+                   "gemms": [f"{n}:{m}x{k}x{nn}" for n, m, k, nn, _, _ in layer_shapes(T)],
+                   "pct_int8_peak": round(100 * value / PEAK_INT8_TOPS, 2), "wall_s": round(wall, 3)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "details": details,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,70 @@
+"""The C-ABI library loads and exports every entry point of include/voxrt_hip.h; host-side argument checks fail
+with the documented status and message (no GPU work: these run on a CPU-only host)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import voxrt_amd as vx
+from voxrt_amd import kernels
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    names = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", fn)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names |= set(re.findall(r"\b(vx_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    names = _declared_symbols()
+    assert {"vx_gemm_ep", "vx_gemm_rows_range", "vx_quantize", "vx_tmat_upload_packed"} <= names
+    L = vx.lib()
+    for n in sorted(names):
+        assert hasattr(L, n), f"{n} declared in include/ but not exported"
+
+
+def test_detect_without_device_reports_scalar():
+    if os.environ.get("HIP_VISIBLE_DEVICES", None) == "" or not vx.lib().vx_detect():
+        assert vx.detect() == vx.Kernel.Scalar
+
+
+def test_upload_rejects_bad_shapes():
+    q = np.zeros((4, (128 + 4) // 5), np.uint8)
+    s = np.zeros((4, 4), np.uint16)
+    with pytest.raises(vx.HipError) as e:
+        vx.TernaryMatrix.from_packed(q, s, 4, 128, 32)  # group not a multiple of 64
+    assert e.value.status == kernels.VX_ERR_INVALID and "group" in str(e.value)
+    h = C.c_void_p()
+    st = vx.lib().vx_tmat_upload_packed(None, None, 4, 128, 128, C.byref(h))
+    assert st == kernels.VX_ERR_INVALID and b"NULL" in vx.lib().vx_last_error()
+    st = vx.lib().vx_tmat_upload_i8(None, None, 4, 100, 50, C.byref(h))
+    assert st == kernels.VX_ERR_INVALID
+
+
+def test_gemm_rejects_null_arguments():
+    st = vx.lib().vx_gemm_ep(None, None, None, None, 1, None, None, 0, 0.0, None, None)
+    assert st == kernels.VX_ERR_INVALID and b"NULL" in vx.lib().vx_last_error()
+    st = vx.lib().vx_quantize(None, 1, 128, 128, None, None, None, None)
+    assert st == kernels.VX_ERR_INVALID
+
+
+def test_last_error_is_cleared_by_success():
+    assert vx.lib().vx_tmat_info(None, None, None, None, None) == kernels.VX_ERR_INVALID
+    assert vx.lib().vx_last_error() != b""
+    # a successful call (an empty quantize is a no-op) clears it
+    assert vx.lib().vx_quantize(C.c_void_p(8), 0, 128, 128, C.c_void_p(8), C.c_void_p(8), None, None) == 0
+    assert vx.lib().vx_last_error() == b""
+
+
+def test_epilogue_values_match_header():
+    hdr = open(os.path.join(ROOT, "include", "voxrt_hip.h")).read()
+    assert "VX_EP_STORE = 0" in hdr and "VX_EP_SILU = 1" in hdr and "VX_EP_ADD_SCALED = 2" in hdr
+    assert vx.Epilogue.Store.kind == 0 and vx.Epilogue.Silu.kind == 1 and vx.Epilogue.AddScaled(0.5).kind == 2

@@ -1,0 +1,326 @@
+"""HIP ternary x int8 GEMM == the oracle, bit for bit (int32 group sums and fp32 outputs), through the C ABI.
+
+Restates the reference's kernel-exactness tests for the HIP backend: crates/voxrt/tests/kernels.rs
+(simd_equals_scalar_exactly, epilogues_are_identical_across_kernels, accumulation_cannot_overflow,
+row_token_ranges_equal_scalar_exactly with its NaN canary) and tests/x86_kernels.rs (ternary and int8 grids, four
+row/token ranges x three epilogues, saturation extremes, the f32-rows operand), plus the quantizer, the stored
+fixtures through the device repack, and the benchmark shapes.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from voxrt_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+FIX = os.path.join(os.path.dirname(__file__), "golden", "fixtures")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    import voxrt_amd as vx
+
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    assert vx.detect() == vx.Kernel.Hip, "no gfx950 device"
+    vx.kernels.check(vx.lib().vx_init(0))
+    return torch.device("cuda:0")
+
+
+def _t(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def _assert_bits_equal(got, want, what):
+    g, w = _bits(got), _bits(want)
+    bad = np.flatnonzero(g.ravel() != w.ravel())
+    assert bad.size == 0, f"{what}: {bad.size} mismatches, first at {bad[0]}: got {got.ravel()[bad[0]]!r} want {want.ravel()[bad[0]]!r}"
+
+
+def _device_gemm(vx, dev, w, x_f32, group, y_init=None, ep=None, want_gs=False):
+    import torch
+
+    ep = ep or vx.Epilogue.Store
+    xa = vx.QuantAct.quantize(_t(x_f32, dev), group)
+    n = x_f32.shape[0]
+    y = _t(y_init, dev) if y_init is not None else torch.zeros((n, w.out), dtype=torch.float32, device=dev)
+    gs = torch.full((w.inp // group, n, w.out), -7, dtype=torch.int32, device=dev) if want_gs else None
+    vx.gemm_ep(w, xa, y, None, ep, gs)
+    torch.cuda.synchronize()
+    return xa, y.cpu().numpy(), (gs.cpu().numpy() if want_gs else None)
+
+
+def _ep_of(vx, ep_kind, alpha):
+    return {0: vx.Epilogue.Store, 1: vx.Epilogue.Silu}.get(ep_kind) or vx.Epilogue.AddScaled(alpha)
+
+
+# ------------------------------------------------------------------------------------------ quantizer
+
+def test_quantize_equals_oracle(dev, orc):
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(3)
+    for n, inp, group in [(1, 128, 128), (17, 256, 128), (338, 1024, 1024), (338, 1024, 128), (5, 4096, 128),
+                          (3, 384, 384), (8, 640, 128)]:
+        x = synth.ref_acts(rng, n, inp)
+        x[0, :group] = 0.0  # an all-zero group
+        x[-1, 1::7] = np.float32(0.5) * (np.arange(x[-1, 1::7].size) % 5).astype(np.float32)  # ties after scaling
+        qa = vx.QuantAct.quantize(_t(x, dev), group)
+        q, s, g = orc.quantize(x, group)
+        np.testing.assert_array_equal(qa.x.cpu().numpy(), q)
+        _assert_bits_equal(qa.scales.cpu().numpy(), s, f"scales n={n} inp={inp} g={group}")
+        np.testing.assert_array_equal(qa.gsum.cpu().numpy(), g)
+
+
+# ------------------------------------------------------------------------------------------ kernels.rs
+
+@pytest.mark.parametrize("out,inp", [(7, 128), (9, 256), (64, 1024), (130, 4096)])
+def test_hip_equals_scalar_exactly(dev, orc, out, inp):
+    """kernels.rs:35-53 (simd_equals_scalar_exactly) for the HIP kernel, plus the int32 group sums."""
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(42 + out)
+    qw, s16, trits = synth.ref_random_matrix(rng, out, inp)
+    w = vx.TernaryMatrix.from_packed(qw, s16, out, inp, 128)
+    ws = orc.f16_to_f32(s16)
+    for n in [1, 3, 4, 5, 17]:
+        x = synth.ref_acts(rng, n, inp)
+        q, xs, _ = orc.quantize(x, 128)
+        want, want_gs = orc.gemm(trits, ws, q, xs, 128, want_group_sums=True)
+        _, got, got_gs = _device_gemm(vx, dev, w, x, 128, want_gs=True)
+        np.testing.assert_array_equal(got_gs, want_gs, err_msg=f"group sums out={out} inp={inp} n={n}")
+        _assert_bits_equal(got, want, f"y out={out} inp={inp} n={n}")
+
+
+def test_epilogues_are_identical(dev, orc):
+    """kernels.rs:91-112: Store, Silu, AddScaled(0.5) on a pre-filled y."""
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(5)
+    out, inp, n = 64, 1024, 13
+    qw, s16, trits = synth.ref_random_matrix(rng, out, inp)
+    w = vx.TernaryMatrix.from_packed(qw, s16, out, inp, 128)
+    ws = orc.f16_to_f32(s16)
+    x = synth.ref_acts(rng, n, inp)
+    q, xs, _ = orc.quantize(x, 128)
+    base = ((np.arange(n * out) % 7) - 3).astype(np.float32).reshape(n, out)
+    for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
+        want = orc.gemm(trits, ws, q, xs, 128, y=base.copy(), ep=ep_kind, alpha=alpha)
+        _, got, _ = _device_gemm(vx, dev, w, x, 128, y_init=base, ep=_ep_of(vx, ep_kind, alpha))
+        _assert_bits_equal(got, want, f"epilogue {ep_kind}")
+
+
+def test_accumulation_cannot_overflow(dev):
+    """kernels.rs:176-200: all +1 trits, x = 127, K = 4096, unit scales -> 4096 * 127."""
+    import voxrt_amd as vx
+
+    inp = 4096
+    qw = synth.pack_rows(np.ones((1, inp), np.int8))
+    s16 = np.full((1, inp // 128), np.float16(1.0)).view(np.uint16)
+    w = vx.TernaryMatrix.from_packed(qw, s16, 1, inp, 128)
+    _, y, gs = _device_gemm(vx, dev, w, np.full((1, inp), 127.0, np.float32), 128, want_gs=True)
+    assert y[0, 0] == 4096 * 127.0
+    assert (gs == 128 * 127).all()
+
+
+def test_bias_is_added_after_epilogue(dev, orc):
+    """gemm_ep adds the bias after the epilogue (kernels/mod.rs:355-361)."""
+    import torch
+
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(17)
+    out, inp, n = 96, 256, 9
+    qw, s16, trits = synth.ref_random_matrix(rng, out, inp)
+    w = vx.TernaryMatrix.from_packed(qw, s16, out, inp, 128)
+    x = synth.ref_acts(rng, n, inp)
+    bias = (rng.take(out) % 100).astype(np.float32) / np.float32(10.0)
+    q, xs, _ = orc.quantize(x, 128)
+    want = orc.gemm(trits, orc.f16_to_f32(s16), q, xs, 128, ep=1)
+    want = (want + bias[None, :]).astype(np.float32)
+    xa = vx.QuantAct.quantize(_t(x, dev), 128)
+    y = torch.zeros((n, out), dtype=torch.float32, device=dev)
+    vx.gemm_ep(w, xa, y, _t(bias, dev), vx.Epilogue.Silu)
+    _assert_bits_equal(y.cpu().numpy(), want, "bias")
+
+
+@pytest.mark.parametrize("out,inp,n", [(14, 128, 11), (34, 128, 19), (8, 256, 8), (6, 128, 3)])
+def test_row_token_ranges_with_nan_canary(dev, orc, out, inp, n):
+    """kernels.rs:202-269: int8 (from_f32_rows) weights, every (row range, token range) equals the scalar kernel
+    and nothing outside the block is written."""
+    import torch
+
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(7 + out)
+    wf = synth.ref_acts(rng, out, inp)
+    wq, wsc, _ = orc.quantize(wf, 128)  # from_f32_rows = per (row, group) absmax quantization
+    w = vx.TernaryMatrix.from_i8_rows(wq, wsc, out, inp, 128)
+    x = synth.ref_acts(rng, n, inp)
+    q, xs, _ = orc.quantize(x, 128)
+    want = orc.gemm(wq, wsc, q, xs, 128)
+    xa = vx.QuantAct.quantize(_t(x, dev), 128)
+    for r0, r1 in [(0, out), (2, out), (0, (out // 2) & ~1), (4, min(6, out))]:
+        for t0, t1 in [(0, n), (0, min(n, 8)), (min(8, n) & ~1, n), (min(2, n), min(n, 5))]:
+            if r0 >= r1 or t0 >= t1:
+                continue
+            y = torch.full((n, out), float("nan"), dtype=torch.float32, device=dev)
+            vx.gemm_rows_range(w, xa, y, r0, r1, t0, t1)
+            got = y.cpu().numpy()
+            inside = np.zeros((n, out), bool)
+            inside[t0:t1, r0:r1] = True
+            assert (np.isnan(got) == ~inside).all(), f"stray write rows {r0}..{r1} toks {t0}..{t1}"
+            _assert_bits_equal(got[inside], want[inside], f"rows {r0}..{r1} toks {t0}..{t1}")
+
+
+# ------------------------------------------------------------------------------------------ x86_kernels.rs
+
+def _check_ranges(vx, dev, orc, rng, w, rows, ws, group, x):
+    import torch
+
+    out, inp = rows.shape
+    n = x.shape[0]
+    q, xs, _ = orc.quantize(x, group)
+    xa = vx.QuantAct.quantize(_t(x, dev), group)
+    ranges = [(0, out, 0, n), (min(1, out), out, 0, n), (0, min(out, 17), n // 2, n),
+              (out // 3, out - out // 4, 0, (n + 1) // 2)]
+    for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.37)]:
+        for r0, r1, t0, t1 in ranges:
+            if r0 >= r1 or t0 >= t1:
+                continue
+            init = ((rng.take(n * out) % 100).astype(np.float32) * np.float32(0.01)).reshape(n, out)
+            want = init.copy()
+            orc.gemm_scalar_range(rows, ws, q, xs, group, want, r0, r1, t0, t1, ep_kind, alpha)
+            y = _t(init, dev)
+            vx.gemm_rows_range(w, xa, y, r0, r1, t0, t1, _ep_of(vx, ep_kind, alpha))
+            _assert_bits_equal(y.cpu().numpy(), want, f"out={out} inp={inp} g={group} n={n} {r0}..{r1} {t0}..{t1} ep={ep_kind}")
+
+
+def test_x86_grid_ternary(dev, orc):
+    """x86_kernels.rs:140-152 grid on the HIP kernel."""
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(3)
+    for out, inp in [(7, 128), (16, 256), (33, 1024), (130, 4096)]:
+        qw, s16, trits = synth.ref_random_matrix(rng, out, inp)
+        w = vx.TernaryMatrix.from_packed(qw, s16, out, inp, 128)
+        for n in [1, 2, 3, 4, 5, 8, 9, 17]:
+            _check_ranges(vx, dev, orc, rng, w, trits, orc.f16_to_f32(s16), 128, synth.ref_acts(rng, n, inp))
+
+
+def test_x86_grid_int8(dev, orc):
+    """x86_kernels.rs:154-172: arbitrary int8 weights, groups 128 / 384 / 1024."""
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(5)
+    for out, inp, group in [(7, 128, 128), (40, 640, 128), (128, 384, 384), (19, 1024, 1024)]:
+        rows = ((rng.take(out * inp) % 255).astype(np.int32) - 127).astype(np.int8).reshape(out, inp)
+        ws = (np.float32(0.001) + (rng.take(out * (inp // group)) % 1000).astype(np.float32) * np.float32(1e-5))
+        ws = ws.astype(np.float32).reshape(out, inp // group)
+        w = vx.TernaryMatrix.from_i8_rows(rows, ws, out, inp, group)
+        for n in [1, 2, 5, 8, 11]:
+            _check_ranges(vx, dev, orc, rng, w, rows, ws, group, synth.ref_acts(rng, n, inp))
+
+
+def test_x86_extremes_do_not_saturate(dev, orc):
+    """x86_kernels.rs:174-185."""
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(9)
+    trits = np.ones((32, 1024), np.int8)
+    s16 = (np.float32(0.01) + (rng.take(32 * 8) % 100).astype(np.float32) * np.float32(0.001)).astype(np.float16)
+    s16 = s16.view(np.uint16).reshape(32, 8)
+    w = vx.TernaryMatrix.from_packed(synth.pack_rows(trits), s16, 32, 1024, 128)
+    x = np.where(np.arange(5 * 1024) % 2 == 0, 5.0, -5.0).astype(np.float32).reshape(5, 1024)
+    _check_ranges(vx, dev, orc, rng, w, trits, orc.f16_to_f32(s16), 128, x)
+    rows = np.where(np.arange(32 * 1024) % 2 == 0, 127, -127).astype(np.int8).reshape(32, 1024)
+    ws = np.full((32, 1), 0.002, np.float32)
+    w8 = vx.TernaryMatrix.from_i8_rows(rows, ws, 32, 1024, 1024)
+    _check_ranges(vx, dev, orc, rng, w8, rows, ws, 1024, x)
+
+
+# ------------------------------------------------------------------------------------------ fixtures
+
+def test_fixture_rows_through_device_repack(dev, orc):
+    """The reference's stored model rows (fixtures_trits.rs) uploaded in their on-disk format: the GEMM against
+    one-hot activations returns the stored dequantised weights exactly, and random activations match the oracle."""
+    import torch
+
+    import voxrt_amd as vx
+
+    meta = json.load(open(os.path.join(FIX, "ternary_fixtures.json")))
+    for tag, m in meta.items():
+        rows, inf, g = m["rows"], m["in_features"], m["group_size"]
+        q = np.fromfile(os.path.join(FIX, f"{tag}.qweight.bin"), np.uint8).reshape(rows, -1)
+        s = np.fromfile(os.path.join(FIX, f"{tag}.scales.f16.bin"), np.uint16).reshape(rows, -1)
+        want_w = np.fromfile(os.path.join(FIX, f"{tag}.weight.f32.bin"), np.float32).reshape(rows, inf)
+        trits = np.fromfile(os.path.join(FIX, f"{tag}.trits.i8.bin"), np.int8).reshape(rows, inf)
+        w = vx.TernaryMatrix.from_packed(q, s, rows, inf, g)
+        # one-hot token c has code 127 at column c and scale 1/127*... use x = 127 * e_c: s = 1, code 127
+        eye = np.zeros((inf, inf), np.float32)
+        eye[np.arange(inf), np.arange(inf)] = 127.0
+        xa = vx.QuantAct.quantize(_t(eye, dev), g)
+        y = torch.zeros((inf, rows), dtype=torch.float32, device=dev)
+        vx.gemm(w, xa, y)
+        got = y.cpu().numpy().T / np.float32(127.0)
+        _assert_bits_equal(got.astype(np.float32), want_w, f"{tag} one-hot")
+        rng = synth.Lcg(77)
+        x = synth.ref_acts(rng, 19, inf)
+        qq, xs, _ = orc.quantize(x, g)
+        want = orc.gemm(trits, orc.f16_to_f32(s), qq, xs, g)
+        _, got, _ = _device_gemm(vx, dev, w, x, g)
+        _assert_bits_equal(got, want, f"{tag} random")
+
+
+# ------------------------------------------------------------------------------------------ workload shapes
+
+def _workload(orc, m, k, n_out, group, seed_cfg=0):
+    trits = synth.synth_trits(synth.workload_seed(seed_cfg, 1), n_out, k)
+    s16 = synth.synth_channel_scales_f16(synth.workload_seed(seed_cfg, 2), n_out, k // group)
+    x = synth.synth_normal(synth.workload_seed(seed_cfg, 3), m * k).reshape(m, k)
+    return trits, s16, x
+
+
+@pytest.mark.parametrize("group", [1024, 128])
+def test_ffn_up_t338_bit_exact(dev, orc, group):
+    """The FFN up-projection of one layer at T=338 (M=338, K=1024, N=4096): per-channel scales with G=K (fp32
+    scale upload) and the model's G=128 (f16 scales): int32 sums and fp32 outputs bit-exact."""
+    import voxrt_amd as vx
+
+    m, k, n_out = 338, 1024, 4096
+    trits, s16, x = _workload(orc, m, k, n_out, group)
+    ws = orc.f16_to_f32(s16)
+    qw = synth.pack_rows(trits)
+    w = vx.TernaryMatrix.from_packed_f32(qw, ws, n_out, k, group) if group == k else \
+        vx.TernaryMatrix.from_packed(qw, s16, n_out, k, group)
+    q, xs, _ = orc.quantize(x, group)
+    want, want_gs = orc.gemm(trits, ws, q, xs, group, want_group_sums=True)
+    _, got, got_gs = _device_gemm(vx, dev, w, x, group, want_gs=True)
+    np.testing.assert_array_equal(got_gs, want_gs)
+    _assert_bits_equal(got, want, f"T=338 FFN-up G={group}")
+
+
+@pytest.mark.parametrize("k,n_out", [(1024, 4096), (4096, 1024)])
+def test_batched_m8192_sampled_rows(dev, orc, k, n_out):
+    """M=8192 (the batched regime): 96 sampled tokens and every output row against the oracle, bit-exact."""
+    import voxrt_amd as vx
+
+    m = 8192
+    trits, s16, x = _workload(orc, m, k, n_out, 128, seed_cfg=2)
+    w = vx.TernaryMatrix.from_packed(synth.pack_rows(trits), s16, n_out, k, 128)
+    _, got, _ = _device_gemm(vx, dev, w, x, 128)
+    pick = np.sort(np.random.default_rng(0).choice(m, 96, replace=False))
+    pick[-1] = m - 1
+    q, xs, _ = orc.quantize(x[pick], 128)
+    want = orc.gemm(trits, orc.f16_to_f32(s16), q, xs, 128)
+    _assert_bits_equal(got[pick], want, f"M=8192 K={k} N={n_out} sampled")

@@ -1,0 +1,92 @@
+// vx_internal.h — shared host and device definitions of libvoxrt_hip (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+
+#include "../../include/voxrt_hip.h"
+
+namespace vx {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Device weight matrix. Ternary matrices hold 2-bit codes (trit + 1) in the MFMA operand order; int8 matrices
+// hold the bytes themselves in the same block order. Rows are padded to a multiple of kRowPad with zero weights
+// and zero scales, so every workgroup column tile reads inside the allocation.
+constexpr int kRowPad = 256;
+
+struct TMat {
+    int64_t out = 0, inp = 0, group = 0, ng = 0, out_pad = 0;
+    bool ternary = false;
+    // ternary: uint32 [out_pad/16][inp/64][64]: lane l = 16*j + n holds the 16 codes of row 16*nb + n at columns
+    //          64*kb + 16*j + 4*d + b, code at bit 8*b + 2*d.
+    // int8:    int8 [out_pad/16][inp/64][64][16]: lane l = 16*j + n holds row 16*nb + n, columns 64*kb + 16*j + i.
+    void *wdev = nullptr;
+    float *scales_t = nullptr;  // float32 [ng][out_pad]
+};
+
+// Error carrying a status code; converted to (status, vx_last_error text) at the ABI boundary.
+struct Error : std::runtime_error {
+    vx_status code;
+    Error(vx_status c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+inline void hip_check(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw Error(VX_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+inline void require(bool ok, const std::string &msg) {
+    if (!ok) throw Error(VX_ERR_INVALID, msg);
+}
+
+// --- device helpers -------------------------------------------------------------------------------------------
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    // gfx9 buffer descriptor, raw (stride 0): loads at byte offsets >= bytes return zero.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ inline float bits_f32(uint32_t u) { return __uint_as_float(u); }
+
+// exp_poly (crates/voxrt/src/tensor.rs:829-848): clamp to [-87, 88], n = rint(x * log2 e), two fma reduction
+// steps, degree-6 Horner by fma, times 2^n. Each step is one IEEE operation (the library is built with
+// -ffp-contract=off), so the result equals the reference bit for bit.
+__device__ inline float exp_poly(float x) {
+    x = x < -87.0f ? -87.0f : x;
+    x = x > 88.0f ? 88.0f : x;
+    float n = __builtin_rintf(x * 1.44269504088896340736f);
+    float r = __builtin_fmaf(-n, 0.69314575f, x);
+    r = __builtin_fmaf(-n, 1.4286068e-6f, r);
+    float p = 1.0f / 720.0f;
+    p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return p * bits_f32((uint32_t)(((int32_t)n + 127) << 23));
+}
+
+// silu_fast / sigmoid_fast (tensor.rs:852-860), IEEE division.
+__device__ inline float silu_fast(float x) { return x / (1.0f + exp_poly(-x)); }
+__device__ inline float sigmoid_fast(float x) { return 1.0f / (1.0f + exp_poly(-x)); }
+
+// Epilogue::apply (kernels/mod.rs:41-48).
+__device__ inline float ep_apply(int ep, float alpha, float old, float v) {
+    if (ep == VX_EP_SILU) return silu_fast(v);
+    if (ep == VX_EP_ADD_SCALED) return __builtin_fmaf(alpha, v, old);
+    return v;
+}
+
+}  // namespace vx
+
+// The public opaque handle (include/voxrt_hip.h) is a shell around the matrix.
+struct vx_tmat {
+    vx::TMat m;
+};
