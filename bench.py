@@ -7,7 +7,8 @@ stacked q|k|v 1024->3072, pos 1024->1024 on 2T-1=675 rows, out-proj 1024->1024 (
 scales in [0.01, 0.05]; activations N(0,1) quantized per token (group = K). value = ternary x int8 GEMM TOPS
 (2*M*N*K per GEMM, zeros counted) over the timed steps.
 
-Prints one JSON line. Extra keys: "roofline" for the dominant kernel (HIP-event time per launch on the launch
+Each step is replayed from a HIP graph captured once (the launches of a real encoder step are captured the same
+way), so the timed region holds device work only. Prints one JSON line. Extra keys: "roofline" for the dominant kernel (HIP-event time per launch on the launch
 stream), "cpu_baseline" (the AVX-512 VNNI restatement on the host cores, bounded sample), "details" (the M=338 and
 M=8192 FFN-up GEMM alone, group = K and 128).
 """
@@ -73,18 +74,39 @@ class Gemm:
         self.vx.gemm_ep(self.w, self.xa, self.y, None, self.ep)
 
 
-def time_launches(torch, gemms, reps):
-    """Average HIP-event time per launch of each GEMM, on torch's current stream (the launch stream)."""
-    st = torch.cuda.current_stream()
+def capture(torch, fn, reps=1):
+    """A HIP graph (torch.cuda.CUDAGraph) replaying `fn` `reps` times: the step is launched back to back by the
+    device, without Python or launch overhead between kernels."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()  # warm (first-call work happens outside the capture)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_launches(torch, gemms, reps, replays=5):
+    """Average device time per launch of each GEMM: a graph of `reps` launches replayed `replays` times, timed
+    with HIP events on the replay stream."""
     out = {}
+    st = torch.cuda.current_stream()
     for g in gemms:
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for a, b in ev:
-            a.record(st)
-            g.run()
-            b.record(st)
+        graph = capture(torch, g.run, reps)
+        graph.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(replays):
+            graph.replay()
+        b.record(st)
         torch.cuda.synchronize()
-        out[g.name] = float(np.mean([a.elapsed_time(b) for a, b in ev])) * 1e-3  # seconds
+        out[g.name] = a.elapsed_time(b) * 1e-3 / (reps * replays)
+        del graph
     return out
 
 
@@ -164,22 +186,24 @@ def main():
         for g in gemms:
             g.run()
 
+    graph = capture(torch, step)
     for _ in range(args.warmup):
-        step()
+        graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(args.steps):
-        step()
+        graph.replay()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_s = e0.elapsed_time(e1) * 1e-3
     ops = sum(g.ops for g in gemms)
     value = ops * args.steps / gpu_s / 1e12
+    del graph
 
-    per = time_launches(torch, gemms, 50)
+    per = time_launches(torch, gemms, 20)
     dom = max(gemms, key=lambda g: per[g.name])
     roof = roofline_of(dom, per[dom.name])
     roof["kernel"] = f"tgemm_kernel ({dom.name}: M={dom.m} K={dom.k} N={dom.n} G={dom.group})"
@@ -194,10 +218,7 @@ def main():
                                    ("ffn_down_m8192_gK", 8192, 4096, 1024, 4096),
                                    ("ffn_down_m8192_g128", 8192, 4096, 1024, 128)]:
             extra.append(Gemm(vx, synth, dev, name, m, k, n, 0, 0.0, grp, 0, 1))
-        for g in extra:
-            for _ in range(5):
-                g.run()
-        pe = time_launches(torch, extra, 30)
+        pe = time_launches(torch, extra, 10)
         for g in extra:
             s = pe[g.name]
             details[g.name] = {"us": round(s * 1e6, 2), "tops": round(g.ops / s / 1e12, 1),

@@ -20,7 +20,7 @@
  * ordered on that stream and returns before the work completes. Calls on different streams that write disjoint
  * outputs may run concurrently; a vx_tmat is immutable after upload and may be shared by any number of calls.
  *
- * Shape rules: inp % group == 0, group % 64 == 0 (one i8 MFMA step is 64 columns), inp >= 64.
+ * Shape rules: inp % group == 0, group % 64 == 0 (one i8 MFMA step is 64 columns).
  */
 #ifndef VOXRT_HIP_H
 #define VOXRT_HIP_H
@@ -72,23 +72,28 @@ void vx_tmat_free(vx_tmat *w);
 
 vx_status vx_tmat_info(const vx_tmat *w, int64_t *out, int64_t *inp, int64_t *group, int *ternary);
 
+/* Padded token count of the transposed activation tables: n rounded up to a multiple of 16. */
+#define VX_NPAD(n) ((((n) + 15) / 16) * 16)
+
 /* quantize_layout on the device: per (token, group) s = absmax/127 (1 when all zero), codes
- * clamp(rint(x * (1/s)), -127, 127); x float32 [n, inp] -> q int8 [n, inp], scales float32 [n, inp/group] and
- * gsum int32 [n, inp/group] (sum of the codes of each group, needed by ternary GEMMs; may be NULL otherwise). */
-vx_status vx_quantize(const float *x, int64_t n, int64_t inp, int64_t group, int8_t *q, float *scales,
-                      int32_t *gsum, void *stream);
+ * clamp(rint(x * (1/s)), -127, 127); x float32 [n, inp] -> q int8 [n, inp], scales_t float32 [inp/group, np] and
+ * gsum_t int32 [inp/group, np] with np = VX_NPAD(n): the scales and code sums transposed (QuantAct::scales_t,
+ * packed.rs:294), pad tokens zero. gsum (sum of the codes of each group) is what ternary GEMMs need. */
+vx_status vx_quantize(const float *x, int64_t n, int64_t inp, int64_t group, int8_t *q, float *scales_t,
+                      int32_t *gsum_t, void *stream);
 
 /* gemm_ep: y[t*out + o] = ep(y_old, sum_g fma-fold of S_g * (xs[t][g] * ws[o][g])) for all t < n, o < out, then
- * y += bias[o] when bias is not NULL. xq int8 [n, inp], xs float32 [n, inp/group], xgsum int32 [n, inp/group]
- * (required for ternary weights), y float32 [n, out]. When group_sums is not NULL the exact int32 group sums S_g
- * are also written to group_sums[(g*n + t)*out + o] (int32 [inp/group, n, out]). */
-vx_status vx_gemm_ep(const vx_tmat *w, const int8_t *xq, const float *xs, const int32_t *xgsum, int64_t n, float *y,
-                     const float *bias, int ep, float alpha, int32_t *group_sums, void *stream);
+ * y += bias[o] when bias is not NULL. xq int8 [n, inp]; xs_t float32 [inp/group, VX_NPAD(n)] and xgsum_t int32
+ * [inp/group, VX_NPAD(n)] as written by vx_quantize (xgsum_t is required for ternary weights); y float32
+ * [n, out]. When group_sums is not NULL the exact int32 group sums S_g are also written to
+ * group_sums[(g*n + t)*out + o] (int32 [inp/group, n, out]). */
+vx_status vx_gemm_ep(const vx_tmat *w, const int8_t *xq, const float *xs_t, const int32_t *xgsum_t, int64_t n,
+                     float *y, const float *bias, int ep, float alpha, int32_t *group_sums, void *stream);
 
 /* gemm_rows_range: as vx_gemm_ep without bias, writing only rows o in [r0, r1) and tokens t in [t0, t1) of
  * y [n, out]; nothing else in y is read or written. */
-vx_status vx_gemm_rows_range(const vx_tmat *w, const int8_t *xq, const float *xs, const int32_t *xgsum, int64_t n,
-                             float *y, int64_t r0, int64_t r1, int64_t t0, int64_t t1, int ep, float alpha,
+vx_status vx_gemm_rows_range(const vx_tmat *w, const int8_t *xq, const float *xs_t, const int32_t *xgsum_t,
+                             int64_t n, float *y, int64_t r0, int64_t r1, int64_t t0, int64_t t1, int ep, float alpha,
                              void *stream);
 
 #ifdef __cplusplus

@@ -60,7 +60,7 @@ def test_last_error_is_cleared_by_success():
     assert vx.lib().vx_tmat_info(None, None, None, None, None) == kernels.VX_ERR_INVALID
     assert vx.lib().vx_last_error() != b""
     # a successful call (an empty quantize is a no-op) clears it
-    assert vx.lib().vx_quantize(C.c_void_p(8), 0, 128, 128, C.c_void_p(8), C.c_void_p(8), None, None) == 0
+    assert vx.lib().vx_quantize(C.c_void_p(8), 0, 128, 128, C.c_void_p(8), C.c_void_p(8), C.c_void_p(8), None) == 0
     assert vx.lib().vx_last_error() == b""
 
 

@@ -71,15 +71,19 @@ def test_quantize_equals_oracle(dev, orc):
 
     rng = synth.Lcg(3)
     for n, inp, group in [(1, 128, 128), (17, 256, 128), (338, 1024, 1024), (338, 1024, 128), (5, 4096, 128),
-                          (3, 384, 384), (8, 640, 128)]:
+                          (3, 384, 384), (8, 640, 128), (33, 4096, 4096), (40, 2048, 256), (21, 1024, 64),
+                          (9, 3072, 1024)]:
         x = synth.ref_acts(rng, n, inp)
         x[0, :group] = 0.0  # an all-zero group
         x[-1, 1::7] = np.float32(0.5) * (np.arange(x[-1, 1::7].size) % 5).astype(np.float32)  # ties after scaling
         qa = vx.QuantAct.quantize(_t(x, dev), group)
         q, s, g = orc.quantize(x, group)
         np.testing.assert_array_equal(qa.x.cpu().numpy(), q)
-        _assert_bits_equal(qa.scales.cpu().numpy(), s, f"scales n={n} inp={inp} g={group}")
-        np.testing.assert_array_equal(qa.gsum.cpu().numpy(), g)
+        st, gt = qa.scales_t.cpu().numpy(), qa.gsum_t.cpu().numpy()
+        assert st.shape == (inp // group, (n + 15) // 16 * 16)
+        _assert_bits_equal(np.ascontiguousarray(st[:, :n].T), s, f"scales n={n} inp={inp} g={group}")
+        np.testing.assert_array_equal(gt[:, :n].T, g)
+        assert (st[:, n:] == 0).all() and (gt[:, n:] == 0).all(), "pad tokens must be zero"
 
 
 # ------------------------------------------------------------------------------------------ kernels.rs

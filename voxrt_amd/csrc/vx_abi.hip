@@ -12,9 +12,9 @@ vx_tmat *upload_packed(const uint8_t *qweight, const void *scales, bool scales_f
                        int64_t group);
 vx_tmat *upload_i8(const int8_t *rows, const float *scales, int64_t out, int64_t inp, int64_t group);
 void free_tmat(vx_tmat *h);
-void quantize(const float *x, int64_t n, int64_t inp, int64_t group, int8_t *q, float *scales, int32_t *gsum,
+void quantize(const float *x, int64_t n, int64_t inp, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t,
               hipStream_t stream);
-void gemm(const TMat *w, const int8_t *xq, const float *xs, const int32_t *xg, int64_t n, float *y,
+void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y,
           const float *bias, int ep, float alpha, int32_t *gs, int64_t r0, int64_t r1, int64_t t0, int64_t t1,
           hipStream_t st);
 }  // namespace vx
@@ -119,26 +119,27 @@ vx_status vx_tmat_info(const vx_tmat *w, int64_t *out, int64_t *inp, int64_t *gr
     });
 }
 
-vx_status vx_quantize(const float *x, int64_t n, int64_t inp, int64_t group, int8_t *q, float *scales,
-                      int32_t *gsum, void *stream) {
-    return guarded([&] { vx::quantize(x, n, inp, group, q, scales, gsum, (hipStream_t)stream); });
+vx_status vx_quantize(const float *x, int64_t n, int64_t inp, int64_t group, int8_t *q, float *scales_t,
+                      int32_t *gsum_t, void *stream) {
+    return guarded([&] { vx::quantize(x, n, inp, group, q, scales_t, gsum_t, (hipStream_t)stream); });
 }
 
-vx_status vx_gemm_ep(const vx_tmat *w, const int8_t *xq, const float *xs, const int32_t *xgsum, int64_t n, float *y,
-                     const float *bias, int ep, float alpha, int32_t *group_sums, void *stream) {
+vx_status vx_gemm_ep(const vx_tmat *w, const int8_t *xq, const float *xs_t, const int32_t *xgsum_t, int64_t n,
+                     float *y, const float *bias, int ep, float alpha, int32_t *group_sums, void *stream) {
     return guarded([&] {
         vx::require(w != nullptr, "weight matrix must not be NULL");
         const vx::TMat *m = unwrap(w);
-        vx::gemm(m, xq, xs, xgsum, n, y, bias, ep, alpha, group_sums, 0, m->out, 0, n, (hipStream_t)stream);
+        vx::gemm(m, xq, xs_t, xgsum_t, n, y, bias, ep, alpha, group_sums, 0, m->out, 0, n, (hipStream_t)stream);
     });
 }
 
-vx_status vx_gemm_rows_range(const vx_tmat *w, const int8_t *xq, const float *xs, const int32_t *xgsum, int64_t n,
-                             float *y, int64_t r0, int64_t r1, int64_t t0, int64_t t1, int ep, float alpha,
+vx_status vx_gemm_rows_range(const vx_tmat *w, const int8_t *xq, const float *xs_t, const int32_t *xgsum_t,
+                             int64_t n, float *y, int64_t r0, int64_t r1, int64_t t0, int64_t t1, int ep, float alpha,
                              void *stream) {
     return guarded([&] {
         vx::require(w != nullptr, "weight matrix must not be NULL");
-        vx::gemm(unwrap(w), xq, xs, xgsum, n, y, nullptr, ep, alpha, nullptr, r0, r1, t0, t1, (hipStream_t)stream);
+        vx::gemm(unwrap(w), xq, xs_t, xgsum_t, n, y, nullptr, ep, alpha, nullptr, r0, r1, t0, t1,
+                 (hipStream_t)stream);
     });
 }
 

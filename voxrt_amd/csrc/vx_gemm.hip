@@ -5,14 +5,18 @@
 //   S_g     = sum_{c in group g} w[o, c] * x[t, c]   (exact int32)
 //
 // Work decomposition. A workgroup of 4 wavefronts owns a tile of BM = 16*MT tokens x BN = 4*16*NT output rows;
-// wavefront w owns the BN/4 rows [16*NT*w, 16*NT*(w+1)) of it and all BM tokens. Per 64-column step the
-// workgroup stages the BM x 64 int8 activation tile in LDS (double buffered, XOR-swizzled 16-byte chunks so a
-// 16-lane phase of ds_read_b128 touches 64 distinct banks) and each wavefront streams its own weight operands
-// straight from HBM into registers: one dword of 2-bit codes per lane per 16x64 block, widened to int8 codes
-// (trit + 1 in {0, 1, 2}) with four shift/and operations. v_mfma_i32_16x16x64_i8 accumulates
-// sum x * (trit + 1) in int32; seeding its C operand with -sum(x) of the group (the quantizer's gsum) makes the
-// accumulator exactly S_g at no extra instruction. At the end of each group the int32 sums are folded into the
-// fp32 accumulators with the reference's operation order; the epilogue applies Store / SiLU / AddScaled (+ bias).
+// wavefront w owns the BN/4 rows [16*NT*w, 16*NT*(w+1)) of it and all BM tokens. The K dimension is walked in
+// 64-column steps. Each step's operands travel through a register ring D steps deep (loads for step kb + D are
+// issued while step kb computes): the BM x 64 int8 activation tile, this wavefront's weight operands (one dword of
+// 2-bit codes per lane per 16x64 block) and, on a group's first step, the group's activation scales, activation
+// code sums and weight scales. One step ahead of use the activation tile is written to LDS (double buffered,
+// XOR-swizzled 16-byte chunks so a 16-lane phase of ds_read_b128 touches 64 distinct banks) and the group's
+// scales to a two-slot LDS table; one barrier per step. The weight codes (trit + 1 in {0, 1, 2}) are widened to
+// int8 with four shift/and operations and v_mfma_i32_16x16x64_i8 accumulates sum x * (trit + 1) in int32;
+// seeding its C operand with -sum(x) of the group (the quantizer's gsum) makes the accumulator exactly S_g at no
+// extra instruction. At the end of each group the int32 sums are folded into the fp32 accumulators in the
+// reference's operation order (a single group, G = K, skips the fp32 accumulator: acc = fma(S, p, 0)); the
+// epilogue applies Store / SiLU / AddScaled (+ bias).
 //
 // MFMA operand layouts (16x16x64, wave64): lane l supplies row l%16 of A and column l%16 of B over the same 16
 // columns of the 64-column step (lane group l/16); D element e of lane l is D[4*(l/16) + e][l%16].
@@ -22,6 +26,8 @@
 // Ragged edges: every read-only operand goes through a raw buffer descriptor whose range ends at the operand's
 // size, so loads past the last token (or past the padded weight rows) return zero without branches; stores are
 // guarded by the [t0, t1) x [r0, r1) window.
+#include <cstring>
+
 #include "vx_internal.h"
 
 namespace vx {
@@ -30,16 +36,17 @@ struct GemmArgs {
     const void *w;          // ternary: uint32 codes; int8: 16-byte chunks (see TMat)
     const float *ws_t;      // [ng][out_pad]
     const int8_t *xq;       // [n][inp]
-    const float *xs;        // [n][ng]
-    const int32_t *xg;      // [n][ng] (ternary only)
+    const float *xs;        // scales_t [ng][np]
+    const int32_t *xg;      // gsum_t [ng][np] (ternary only)
     float *y;               // [n][out]
     const float *bias;      // [out] or NULL
     int32_t *gs;            // [ng][n][out] or NULL
-    int64_t n, out, inp, ng, out_pad, spg;
-    int64_t r0, r1, t0, t1, n_base;
+    int64_t n, np, out, inp, ng, out_pad, spg;
+    int64_t r0, r1, t0, t1, n_base, m_base;
     uint32_t w_bytes, ws_bytes, xq_bytes, xs_bytes;
     int ep;
     float alpha;
+    int vec_ok;  // y (and bias) rows are 16-byte aligned: out % 4 == 0 and 16-byte aligned base pointers
 };
 
 __device__ inline v4i widen_codes(uint32_t p) {
@@ -51,146 +58,202 @@ __device__ inline v4i widen_codes(uint32_t p) {
     return r;
 }
 
-template <int MT, int NT, bool TERN, bool GS>
+// int32 group sums of group g to gs[(g*n + t)*out + o] inside the [t0, t1) x [r0, r1) window
+template <int MT, int NT>
+__device__ inline void store_group_sums(const GemmArgs &a, const v4i (&acc)[MT][NT], int g, int m0, int nw0, int aj,
+                                        int arow) {
+#pragma unroll
+    for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int64_t t = m0 + mb * 16 + 4 * aj + e;
+            if (t < a.t0 || t >= a.t1) continue;
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++) {
+                const int64_t o = nw0 + nb * 16 + arow;
+                if (o >= a.r0 && o < a.r1) a.gs[((int64_t)g * a.n + t) * a.out + o] = acc[mb][nb][e];
+            }
+        }
+}
+
+// Epilogue (kernels/mod.rs:41-48; the bias is added after it as in gemm_ep, kernels/mod.rs:355-361), one
+// 16-token block at a time: the old outputs and the bias are loaded in one batch, then each output in the
+// [t0, t1) x [r0, r1) window is written once. A single group folds here: acc = fma(S, xs * ws, 0).
+template <int MT, int NT, bool SINGLE, class XS>
+__device__ inline void epilogue(const GemmArgs &a, const v4i (&acc)[MT][NT],
+                                const float (&accf)[SINGLE ? 1 : MT][SINGLE ? 1 : NT][4], const XS &xsf,
+                                const float (&wsf)[SINGLE ? NT : 1], int m0, int nw0, int aj, int arow) {
+    float bia[NT];
+    const bool add = a.ep == VX_EP_ADD_SCALED;
+#pragma unroll
+    for (int nb = 0; nb < NT; nb++) {
+        const int64_t o = nw0 + nb * 16 + arow;
+        bia[nb] = (a.bias && o >= a.r0 && o < a.r1) ? a.bias[o] : 0.0f;
+    }
+#pragma unroll
+    for (int mb = 0; mb < MT; mb++) {
+        float old[4][NT];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++) {
+                const int64_t t = m0 + mb * 16 + 4 * aj + e, o = nw0 + nb * 16 + arow;
+                old[e][nb] = (add && t >= a.t0 && t < a.t1 && o >= a.r0 && o < a.r1) ? a.y[t * a.out + o] : 0.0f;
+            }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int64_t t = m0 + mb * 16 + 4 * aj + e;
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++) {
+                const int64_t o = nw0 + nb * 16 + arow;
+                if (t < a.t0 || t >= a.t1 || o < a.r0 || o >= a.r1) continue;
+                float v;
+                if constexpr (SINGLE)
+                    v = __builtin_fmaf((float)acc[mb][nb][e], __int_as_float(xsf[mb][e]) * wsf[nb], 0.0f);
+                else
+                    v = accf[mb][nb][e];
+                float r = ep_apply(a.ep, a.alpha, old[e][nb], v);
+                if (a.bias) r = r + bia[nb];
+                a.y[t * a.out + o] = r;
+            }
+        }
+    }
+}
+
+template <int MT, int NT, bool TERN, bool GS, bool SINGLE, int D>
 __global__ __launch_bounds__(256) void tgemm_kernel(const GemmArgs a) {
     constexpr int BM = MT * 16;
     constexpr int BN = NT * 16 * 4;
-    constexpr int ACH = (BM * 4 + 255) / 256;  // 16-byte activation chunks per thread per step
-    __shared__ __attribute__((aligned(16))) int8_t lds[2][BM * 64];
+    constexpr int ACH = (BM * 4 + 255) / 256;  // 16-byte activation chunks per thread per stage
+    constexpr int SW = 2 * BM + BN;            // scale words of one group: xs[BM], gsum[BM], ws[BN]
+    __shared__ __attribute__((aligned(16))) int8_t lds_a[2][BM * 64];
+    __shared__ float lds_s[2][SW];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t m0 = a.t0 + (int64_t)blockIdx.y * BM;
-    const int64_t nw0 = a.n_base + (int64_t)blockIdx.x * BN + wave * NT * 16;
-    const int64_t nk = a.inp / 64;
-    const int64_t ng = a.ng;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int arow = lane & 15, aj = lane >> 4;
+    // 32-bit index arithmetic: the host guarantees every operand is below 4 GiB
+    const int m0 = (int)a.m_base + (int)blockIdx.y * BM;
+    const int nblk0 = (int)a.n_base + (int)blockIdx.x * BN;
+    const int nw0 = nblk0 + wave * NT * 16;
+    const int nk = (int)(a.inp / 64), inp = (int)a.inp, ng = (int)a.ng, spg = (int)a.spg, np = (int)a.np;
+    const int out_pad = (int)a.out_pad;
 
     const auto xrs = make_rsrc(a.xq, a.xq_bytes);
     const auto wrs = make_rsrc(a.w, a.w_bytes);
-    const auto srs = make_rsrc(a.xs, a.xs_bytes);
-    const auto grs = make_rsrc(a.xg, a.xs_bytes);
-    const auto wsrs = make_rsrc(a.ws_t, a.ws_bytes);
+    // the scale operand of this wavefront's role (see issue): activation scales, code sums or weight scales
+    const auto rsrc = make_rsrc(wave == 0 ? (const void *)a.xs : (wave == 1 ? (const void *)a.xg : (const void *)a.ws_t),
+                                wave < 2 ? a.xs_bytes : a.ws_bytes);
 
-    // activation chunk c of a step: row c >> 2, 16-byte column chunk c & 3
-    v4i apre[ACH];
-    auto load_a = [&](int64_t kb) {
+    // Register ring of D stages in flight: stage kb = the 64-column step kb of the activation tile, the weight
+    // operands of this wavefront and, on the first step of a group, that group's scales and code sums. Loads are
+    // issued D steps before use and consumed in issue order, so the in-order vmcnt wait only ever waits for the
+    // oldest stage.
+    typedef typename std::conditional<TERN, uint32_t, v4i>::type BReg;
+    v4i ra[D][ACH];
+    BReg rb[D][NT];
+    uint32_t rs[SINGLE ? 1 : D][2];
+
+    // (group, step within the group) of a stage, advanced by counting instead of dividing
+    struct Pos {
+        int g, s;
+    };
+    auto advance = [&](Pos p) {
+        p.s++;
+        if (p.s == spg) {
+            p.s = 0;
+            p.g++;
+        }
+        return p;
+    };
+
+    // Every lane issues the same loads on every step (a load that is not wanted gets an offset past the end of
+    // its buffer and returns zero without touching memory): with a fixed load count per step the compiler's
+    // in-order vmcnt waits can name exactly the stage that is consumed instead of draining the whole ring.
+    constexpr uint32_t kOff = 0xFFFFFFF0u;
+    auto scale_off = [&](int j, int g) {
+        uint32_t off = kOff;
+        if (wave < 2) {
+            if (j == 0 && lane < BM && (wave == 0 || TERN)) off = (uint32_t)((g * np + m0 + lane) * 4);
+        } else {
+            const int c = (wave - 2) * (BN / 2) + j * 64 + lane;
+            if (j * 64 + lane < BN / 2) off = (uint32_t)((g * out_pad + nblk0 + c) * 4);
+        }
+        return off;
+    };
+    auto issue = [&](int kb, Pos p, int slot) {
+        const bool live = kb < nk;
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
             const int c = tid + i * 256;
-            if (c < BM * 4) {
-                const uint32_t off = (uint32_t)((m0 + (c >> 2)) * a.inp + kb * 64 + (c & 3) * 16);
-                apre[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
-            }
+            const uint32_t off = (uint32_t)((m0 + (c >> 2)) * inp + kb * 64 + (c & 3) * 16);
+            ra[slot][i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, live && c < BM * 4 ? off : kOff, 0, 0);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++) {
+            const uint32_t blk = (uint32_t)((nw0 / 16 + nb) * nk + kb);
+            if constexpr (TERN)
+                rb[slot][nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, live ? (blk * 64 + lane) * 4 : kOff, 0, 0);
+            else
+                rb[slot][nb] = __builtin_amdgcn_raw_buffer_load_b128(wrs, live ? (blk * 64 + lane) * 16 : kOff, 0, 0);
+        }
+        // scale words of the group, one role per wavefront (so the buffer descriptor stays uniform): wave 0 the
+        // activation scales of the BM tokens, wave 1 their code sums, waves 2 and 3 one half each of the BN
+        // weight scales; every wavefront issues the same two loads (a single group loads them once, in the
+        // prologue, outside the ring)
+        if constexpr (!SINGLE) {
+            const bool gl = live && p.s == 0;
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                rs[slot][j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, gl ? scale_off(j, p.g) : kOff, 0, 0);
         }
     };
-    auto store_a = [&](int buf) {
+
+    // ring slot -> LDS: the activation tile (XOR-swizzled 16-byte chunks) and, on a group start, the scales
+    auto store = [&](int slot, int kb, Pos p) {
+        const int buf = kb & 1;
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
             const int c = tid + i * 256;
             if (c < BM * 4) {
                 const int row = c >> 2, ch = (c & 3) ^ ((row >> 2) & 3);
-                *(v4i *)&lds[buf][row * 64 + ch * 16] = apre[i];
+                *(v4i *)&lds_a[buf][row * 64 + ch * 16] = ra[slot][i];
             }
         }
-    };
-
-    // weight operand of block nb of this wavefront at step kb
-    typedef typename std::conditional<TERN, uint32_t, v4i>::type BReg;
-    BReg bcur[NT], bpre[NT];
-    auto load_b = [&](int64_t kb, BReg *dst) {
+        if (p.s == 0) {
+            float *dst = lds_s[p.g & 1];
 #pragma unroll
-        for (int nb = 0; nb < NT; nb++) {
-            const int64_t blk = (nw0 / 16 + nb) * nk + kb;
-            if constexpr (TERN)
-                dst[nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)((blk * 64 + lane) * 4), 0, 0);
-            else
-                dst[nb] = __builtin_amdgcn_raw_buffer_load_b128(wrs, (uint32_t)((blk * 64 + lane) * 16), 0, 0);
+            for (int j = 0; j < 2; j++) {
+                const float v = __builtin_bit_cast(float, rs[SINGLE ? 0 : slot][j]);
+                if (wave < 2) {
+                    if (j == 0 && lane < BM) dst[wave * BM + lane] = v;
+                } else if (j * 64 + lane < BN / 2) {
+                    dst[2 * BM + (wave - 2) * (BN / 2) + j * 64 + lane] = v;
+                }
+            }
         }
     };
 
     v4i acc[MT][NT];
-    float accf[MT][NT][4];
-#pragma unroll
-    for (int mb = 0; mb < MT; mb++)
-#pragma unroll
-        for (int nb = 0; nb < NT; nb++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) accf[mb][nb][e] = 0.0f;
-
-    load_a(0);
-    load_b(0, bcur);
-    store_a(0);
-    __syncthreads();
-
-    const int arow = lane & 15, aj = lane >> 4;
-    int64_t kb = 0;
-    for (int64_t g = 0; g < ng; g++) {
-        v4i cinit[MT];
+    float accf[SINGLE ? 1 : MT][SINGLE ? 1 : NT][4];  // fp32 accumulators (a single group folds in the epilogue)
+    if constexpr (!SINGLE) {
 #pragma unroll
         for (int mb = 0; mb < MT; mb++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                if constexpr (TERN) {
-                    const int64_t t = m0 + mb * 16 + 4 * aj + e;
-                    cinit[mb][e] = -(int)__builtin_amdgcn_raw_buffer_load_b32(grs, (uint32_t)((t * ng + g) * 4), 0, 0);
-                } else {
-                    cinit[mb][e] = 0;
-                }
-            }
-        for (int64_t s = 0; s < a.spg; s++, kb++) {
-            const int buf = (int)(kb & 1);
-            if (kb + 1 < nk) {
-                load_a(kb + 1);
-                load_b(kb + 1, bpre);
-            }
-            v4i av[MT], bv[NT];
+            for (int nb = 0; nb < NT; nb++)
 #pragma unroll
-            for (int mb = 0; mb < MT; mb++) {
-                const int row = mb * 16 + arow, ch = aj ^ ((row >> 2) & 3);
-                av[mb] = *(const v4i *)&lds[buf][row * 64 + ch * 16];
-            }
-#pragma unroll
-            for (int nb = 0; nb < NT; nb++) {
-                if constexpr (TERN)
-                    bv[nb] = widen_codes(bcur[nb]);
-                else
-                    bv[nb] = bcur[nb];
-            }
-            if (s == 0) {
-#pragma unroll
-                for (int mb = 0; mb < MT; mb++)
-#pragma unroll
-                    for (int nb = 0; nb < NT; nb++)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mb], bv[nb], cinit[mb], 0, 0, 0);
-            } else {
-#pragma unroll
-                for (int mb = 0; mb < MT; mb++)
-#pragma unroll
-                    for (int nb = 0; nb < NT; nb++)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mb], bv[nb], acc[mb][nb], 0, 0, 0);
-            }
-            if (kb + 1 < nk) {
-                store_a(buf ^ 1);
-#pragma unroll
-                for (int nb = 0; nb < NT; nb++) bcur[nb] = bpre[nb];
-            }
-            __syncthreads();
-        }
-        // fold group g: acc_f = fma((float)S_g, xs[t][g] * ws[o][g], acc_f)
+                for (int e = 0; e < 4; e++) accf[mb][nb][e] = 0.0f;
+    }
+
+    // fold group g into the fp32 accumulators: acc_f = fma((float)S_g, xs[t][g] * ws[o][g], acc_f)
+    auto fold = [&](int g) {
+        const float *sx = lds_s[g & 1];
         float xsv[MT][4], wsv[NT];
 #pragma unroll
         for (int mb = 0; mb < MT; mb++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int64_t t = m0 + mb * 16 + 4 * aj + e;
-                xsv[mb][e] = __builtin_bit_cast(
-                    float, __builtin_amdgcn_raw_buffer_load_b32(srs, (uint32_t)((t * ng + g) * 4), 0, 0));
-            }
+            for (int e = 0; e < 4; e++) xsv[mb][e] = sx[mb * 16 + 4 * aj + e];
 #pragma unroll
-        for (int nb = 0; nb < NT; nb++) {
-            const int64_t o = nw0 + nb * 16 + arow;
-            wsv[nb] = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(wsrs, (uint32_t)((g * a.out_pad + o) * 4), 0, 0));
-        }
+        for (int nb = 0; nb < NT; nb++) wsv[nb] = sx[2 * BM + wave * NT * 16 + nb * 16 + arow];
 #pragma unroll
         for (int mb = 0; mb < MT; mb++)
 #pragma unroll
@@ -198,107 +261,598 @@ __global__ __launch_bounds__(256) void tgemm_kernel(const GemmArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const float p = xsv[mb][e] * wsv[nb];
-                    accf[mb][nb][e] = __builtin_fmaf((float)acc[mb][nb][e], p, accf[mb][nb][e]);
+                    if constexpr (!SINGLE) accf[mb][nb][e] = __builtin_fmaf((float)acc[mb][nb][e], p, accf[mb][nb][e]);
                 }
-        if constexpr (GS) {
+        if constexpr (GS) store_group_sums<MT, NT>(a, acc, g, m0, nw0, aj, arow);
+    };
+
+    auto compute = [&](int kb, Pos p, int slot) {
+        const int buf = kb & 1;
+        v4i av[MT], bv[NT];
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++) {
+            const int row = mb * 16 + arow, ch = aj ^ ((row >> 2) & 3);
+            av[mb] = *(const v4i *)&lds_a[buf][row * 64 + ch * 16];
+        }
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++) {
+            if constexpr (TERN)
+                bv[nb] = widen_codes(rb[slot][nb]);
+            else
+                bv[nb] = rb[slot][nb];
+        }
+        if (p.s == 0) {
+            // seed C with -sum(x) of the group (ternary codes are trit + 1), so the accumulator ends at S_g
+            const float *sx = lds_s[p.g & 1];
+            v4i cinit[MT];
 #pragma unroll
             for (int mb = 0; mb < MT; mb++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int64_t t = m0 + mb * 16 + 4 * aj + e;
-                    if (t >= a.t1) continue;
+                for (int e = 0; e < 4; e++)
+                    cinit[mb][e] = TERN ? -__builtin_bit_cast(int, sx[BM + mb * 16 + 4 * aj + e]) : 0;
 #pragma unroll
-                    for (int nb = 0; nb < NT; nb++) {
-                        const int64_t o = nw0 + nb * 16 + arow;
-                        if (o >= a.r0 && o < a.r1) a.gs[(g * a.n + t) * a.out + o] = acc[mb][nb][e];
-                    }
+            for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+                for (int nb = 0; nb < NT; nb++)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mb], bv[nb], cinit[mb], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+                for (int nb = 0; nb < NT; nb++)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mb], bv[nb], acc[mb][nb], 0, 0, 0);
+        }
+        if (!SINGLE && p.s == spg - 1) fold(p.g);
+    };
+
+    // D divides nk (the host picks it), so every unrolled step below is a real one
+    Pos pc = {0, 0}, ps = {0, 0}, pi = {0, 0};
+    if constexpr (SINGLE) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) rs[0][j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, scale_off(j, 0), 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+        issue(i, pi, i);
+        pi = advance(pi);
+    }
+    store(0, 0, ps);
+    ps = advance(ps);
+    __syncthreads();
+    for (int kb0 = 0; kb0 < nk; kb0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; i++) {
+            const int kb = kb0 + i;
+            compute(kb, pc, i);
+            pc = advance(pc);
+            if (kb + 1 < nk) store((i + 1) % D, kb + 1, ps);
+            ps = advance(ps);
+            issue(kb + D, pi, i);
+            pi = advance(pi);
+            __syncthreads();
+        }
+    }
+    // a single group folds in the epilogue with the scales staged in LDS slot 0
+    v4i xsf[MT];
+    float wsf[SINGLE ? NT : 1];
+    if constexpr (SINGLE) {
+        const float *sx = lds_s[0];
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) xsf[mb][e] = __builtin_bit_cast(int, sx[mb * 16 + 4 * aj + e]);
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++) wsf[SINGLE ? nb : 0] = sx[2 * BM + wave * NT * 16 + nb * 16 + arow];
+        if constexpr (GS) store_group_sums<MT, NT>(a, acc, 0, m0, nw0, aj, arow);
+    }
+    epilogue<MT, NT, SINGLE>(a, acc, accf, xsf, wsf, m0, nw0, aj, arow);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Direct kernel: every wavefront owns a 16*MT x 16*NT output tile and streams its own operands from memory into
+// registers (the four wavefronts of a workgroup share their activation rows through the L1 cache). There is no
+// LDS staging and no barrier in the K loop, so a wavefront's only wait is for the data of the stage it consumes:
+// the register ring keeps D stages of KS 64-column steps in flight, up to the whole K for the small-token shapes
+// where the kernel is bound by memory latency rather than by MFMA or HBM throughput. A stage is one quantization
+// group (KS = group / 64) and carries the group's activation scales and code sums for the lane's 4 tokens
+// (16-byte loads from the transposed [ng][np] layout) and the weight scales of its NT rows; a single group
+// (G = K) loads its code sums once before the loop and its scales once after it.
+template <int MT, int NT, bool TERN, bool GS, bool SINGLE, int KS, int D>
+__global__ __launch_bounds__(256) void tgemm_direct_kernel(const GemmArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int arow = lane & 15, aj = lane >> 4;
+    const int m0 = (int)a.m_base + (int)blockIdx.y * (MT * 16);
+    const int nw0 = (int)a.n_base + (int)blockIdx.x * (NT * 64) + wave * NT * 16;
+    const int inp = (int)a.inp, nk = inp / 64, nst = nk / KS, np = (int)a.np, out_pad = (int)a.out_pad;
+
+    const auto xrs = make_rsrc(a.xq, a.xq_bytes);
+    const auto wrs = make_rsrc(a.w, a.w_bytes);
+    const auto srs = make_rsrc(a.xs, a.xs_bytes);
+    const auto grs = make_rsrc(a.xg, a.xs_bytes);
+    const auto wsrs = make_rsrc(a.ws_t, a.ws_bytes);
+
+    typedef typename std::conditional<TERN, uint32_t, v4i>::type BReg;
+    constexpr int SD = SINGLE ? 1 : D;  // per-stage scale registers exist only for multi-group GEMMs
+    v4i ra[D][KS][MT];
+    BReg rb[D][KS][NT];
+    v4i rx[SD][MT], rg[SD][MT];  // activation scales / code sums of the lane's 4 tokens per 16-token block
+    float rw[SD][NT];            // weight scale of the lane's output row per 16-row block
+
+    constexpr uint32_t kOff = 0xFFFFFFF0u;
+    // token offset of the lane's 4 scale entries of block mb in the [ng][np] tables
+    auto tok4 = [&](int mb) { return m0 + mb * 16 + 4 * aj; };
+    auto issue = [&](int s, int slot) {
+        const bool live = s < nst;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const int kb = s * KS + ks;
+#pragma unroll
+            for (int mb = 0; mb < MT; mb++) {
+                const uint32_t off = (uint32_t)((m0 + mb * 16 + arow) * inp + kb * 64 + 16 * aj);
+                ra[slot][ks][mb] = __builtin_amdgcn_raw_buffer_load_b128(xrs, live ? off : kOff, 0, 0);
+            }
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++) {
+                const uint32_t blk = (uint32_t)((nw0 / 16 + nb) * nk + kb);
+                if constexpr (TERN)
+                    rb[slot][ks][nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, live ? (blk * 64 + lane) * 4 : kOff,
+                                                                            0, 0);
+                else
+                    rb[slot][ks][nb] = __builtin_amdgcn_raw_buffer_load_b128(
+                        wrs, live ? (blk * 64 + lane) * 16 : kOff, 0, 0);
+            }
+        }
+        if constexpr (!SINGLE) {
+            const int g = s;  // one group per stage
+#pragma unroll
+            for (int mb = 0; mb < MT; mb++) {
+                const uint32_t off = (uint32_t)((g * np + tok4(mb)) * 4);
+                rx[slot][mb] = __builtin_amdgcn_raw_buffer_load_b128(srs, live ? off : kOff, 0, 0);
+                if constexpr (TERN) rg[slot][mb] = __builtin_amdgcn_raw_buffer_load_b128(grs, live ? off : kOff, 0, 0);
+            }
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++) {
+                const uint32_t off = (uint32_t)((g * out_pad + nw0 + nb * 16 + arow) * 4);
+                rw[slot][nb] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsrs, live ? off : kOff, 0, 0));
+            }
+        }
+    };
+
+    v4i acc[MT][NT];
+    float accf[SINGLE ? 1 : MT][SINGLE ? 1 : NT][4];
+    if constexpr (!SINGLE) {
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) accf[mb][nb][e] = 0.0f;
+    }
+
+    // single group: the code sums seed the accumulators once (loaded before the ring, so they are the oldest)
+    v4i g0[SINGLE ? MT : 1];
+    if constexpr (SINGLE) {
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++)
+            g0[mb] = TERN ? __builtin_amdgcn_raw_buffer_load_b128(grs, (uint32_t)(tok4(mb) * 4), 0, 0) : v4i{0, 0, 0, 0};
+    }
+
+    auto compute = [&](int s, int slot) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            v4i bv[NT];
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++) {
+                if constexpr (TERN)
+                    bv[nb] = widen_codes(rb[slot][ks][nb]);
+                else
+                    bv[nb] = rb[slot][ks][nb];
+            }
+            const bool first = ks == 0 && (!SINGLE || s == 0);
+            if (first) {
+                // seed C with -sum(x) of the group (ternary codes are trit + 1), so the accumulator ends at S_g
+#pragma unroll
+                for (int mb = 0; mb < MT; mb++) {
+                    const v4i gsum = SINGLE ? g0[SINGLE ? mb : 0] : rg[SINGLE ? 0 : slot][mb];
+                    const v4i cinit = TERN ? -gsum : v4i{0, 0, 0, 0};
+#pragma unroll
+                    for (int nb = 0; nb < NT; nb++)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ra[slot][ks][mb], bv[nb], cinit, 0, 0, 0);
                 }
+            } else {
+#pragma unroll
+                for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+                    for (int nb = 0; nb < NT; nb++)
+                        acc[mb][nb] =
+                            __builtin_amdgcn_mfma_i32_16x16x64_i8(ra[slot][ks][mb], bv[nb], acc[mb][nb], 0, 0, 0);
+            }
+        }
+        if constexpr (!SINGLE) {
+            // fold group s: acc_f = fma((float)S_g, xs[t][g] * ws[o][g], acc_f)
+#pragma unroll
+            for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+                for (int nb = 0; nb < NT; nb++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float p = __int_as_float(rx[slot][mb][e]) * rw[slot][nb];
+                        accf[mb][nb][e] = __builtin_fmaf((float)acc[mb][nb][e], p, accf[mb][nb][e]);
+                    }
+            if constexpr (GS) store_group_sums<MT, NT>(a, acc, s, m0, nw0, aj, arow);
+        }
+    };
+
+#pragma unroll
+    for (int i = 0; i < D; i++) issue(i, i);
+    for (int s0 = 0; s0 < nst; s0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; i++) {
+            const int s = s0 + i;
+            if (s < nst) compute(s, i);
+            issue(s + D, i);
         }
     }
 
-    // epilogue (kernels/mod.rs:41-48; bias added after it as in gemm_ep, kernels/mod.rs:355-361)
+    // single group: its scales, loaded after the loop
+    v4i xsf[SINGLE ? MT : 1];
+    float wsf[SINGLE ? NT : 1];
+    if constexpr (SINGLE) {
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++) xsf[mb] = __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)(tok4(mb) * 4), 0, 0);
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++)
+            wsf[nb] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                    wsrs, (uint32_t)((nw0 + nb * 16 + arow) * 4), 0, 0));
+        if constexpr (GS) store_group_sums<MT, NT>(a, acc, 0, m0, nw0, aj, arow);
+    }
+    epilogue<MT, NT, SINGLE>(a, acc, accf, xsf, wsf, m0, nw0, aj, arow);
+}
+
+
+// ---------------------------------------------------------------------------------------------------------------
+// Split-K kernel (one group, G = K; the small-token shapes). The four wavefronts of a workgroup share one
+// 16*MT x 16*NT output tile and each walks a quarter of the K steps with up to all of its stages in flight (a
+// register ring D stages deep; the per-step offsets travel in scalar registers, so a step costs no vector address
+// arithmetic, and the loop is peeled so that no load is conditional). Their int32 partial sums meet in LDS, where
+// the sum is exact in any order (wave 0 seeds its MFMA chain with -sum(x) of the tokens, the others with zero).
+// Then each thread owns 8 consecutive outputs of one token: S -> acc = fma(S, xs * ws, 0), the epilogue, and two
+// 16-byte stores.
+template <int MT, int NT, bool TERN, bool GS, int D>
+__global__ __launch_bounds__(256) void tgemm_splitk_kernel(const GemmArgs a) {
+    constexpr int BM = 16 * MT, BN = 16 * NT, BNP = BN + 4;  // BNP: LDS row pitch (bank-conflict-free writes)
+    static_assert(BM * BN == 256 * 8, "each thread folds 8 outputs");
+    __shared__ __attribute__((aligned(16))) int red[4][BM * BNP];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int arow = lane & 15, aj = lane >> 4;
+    const int m0 = (int)a.m_base + (int)blockIdx.y * BM;
+    const int n0 = (int)a.n_base + (int)blockIdx.x * BN;
+    const int inp = (int)a.inp, nk = inp / 64, nkw = nk / 4, kb0 = wave * nkw;
+
+    const auto xrs = make_rsrc(a.xq, a.xq_bytes);
+    const auto wrs = make_rsrc(a.w, a.w_bytes);
+    const auto srs = make_rsrc(a.xs, a.xs_bytes);
+    const auto grs = make_rsrc(a.xg, a.xs_bytes);
+    const auto wsrs = make_rsrc(a.ws_t, a.ws_bytes);
+
+    // lane-constant offsets; a token past n lands past the end of xq and reads zeros
+    int va[MT];
+#pragma unroll
+    for (int mb = 0; mb < MT; mb++) va[mb] = (m0 + mb * 16 + arow) * inp + 16 * aj;
+    constexpr int BBYTES = TERN ? 4 : 16;  // weight operand bytes per lane per 16x64 block
+    const int vb = lane * BBYTES;
+
+    typedef typename std::conditional<TERN, uint32_t, v4i>::type BReg;
+    v4i ra[D][MT];
+    BReg rb[D][NT];
+    auto issue = [&](int kb, int slot) {
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++) ra[slot][mb] = __builtin_amdgcn_raw_buffer_load_b128(xrs, va[mb], kb * 64, 0);
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++) {
+            const int soff = ((n0 / 16 + nb) * nk + kb) * 64 * BBYTES;
+            if constexpr (TERN)
+                rb[slot][nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, vb, soff, 0);
+            else
+                rb[slot][nb] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vb, soff, 0);
+        }
+    };
+
+    // wave 0 seeds its chain with -gsum of the lane's 4 tokens per block; the other waves with zero
+    v4i cinit[MT];
+#pragma unroll
+    for (int mb = 0; mb < MT; mb++) {
+        cinit[mb] = v4i{0, 0, 0, 0};
+        if (TERN && wave == 0)
+            cinit[mb] = -(v4i)__builtin_amdgcn_raw_buffer_load_b128(grs, (m0 + mb * 16 + 4 * aj) * 4, 0, 0);
+    }
+
+    v4i acc[MT][NT];
+    auto compute = [&](int slot, bool first) {
+        v4i bv[NT];
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++) {
+            if constexpr (TERN)
+                bv[nb] = widen_codes(rb[slot][nb]);
+            else
+                bv[nb] = rb[slot][nb];
+        }
+        if (first) {
+#pragma unroll
+            for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+                for (int nb = 0; nb < NT; nb++)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ra[slot][mb], bv[nb], cinit[mb], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+                for (int nb = 0; nb < NT; nb++)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ra[slot][mb], bv[nb], acc[mb][nb], 0, 0, 0);
+        }
+    };
+
+    // D divides nkw (the host picks it): prologue, steady state, drain
+#pragma unroll
+    for (int i = 0; i < D; i++) issue(kb0 + i, i);
+    for (int s0 = 0; s0 < nkw - D; s0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; i++) {
+            compute(i, s0 + i == 0);
+            issue(kb0 + s0 + i + D, i);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < D; i++) compute(i, nkw - D + i == 0);
+
+    // partial sums -> LDS
 #pragma unroll
     for (int mb = 0; mb < MT; mb++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int64_t t = m0 + mb * 16 + 4 * aj + e;
-            if (t >= a.t1) continue;
+        for (int nb = 0; nb < NT; nb++)
 #pragma unroll
-            for (int nb = 0; nb < NT; nb++) {
-                const int64_t o = nw0 + nb * 16 + arow;
-                if (o < a.r0 || o >= a.r1) continue;
-                float *p = a.y + t * a.out + o;
-                float r = ep_apply(a.ep, a.alpha, a.ep == VX_EP_ADD_SCALED ? *p : 0.0f, accf[mb][nb][e]);
-                if (a.bias) r = r + a.bias[o];
-                *p = r;
-            }
+            for (int e = 0; e < 4; e++) red[wave][(mb * 16 + 4 * aj + e) * BNP + nb * 16 + arow] = acc[mb][nb][e];
+    __syncthreads();
+
+    // thread -> token tt of the tile, rows c0 .. c0+7
+    const int tt = tid / (BN / 8), c0 = (tid % (BN / 8)) * 8;
+    int S[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) S[j] = 0;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const v4i lo = *(const v4i *)&red[w][tt * BNP + c0];
+        const v4i hi = *(const v4i *)&red[w][tt * BNP + c0 + 4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            S[j] += lo[j];
+            S[4 + j] += hi[j];
         }
+    }
+    const int t = m0 + tt, o0 = n0 + c0;
+    if (t < a.t0 || t >= a.t1) return;
+    const float xs = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, t * 4, 0, 0));
+    const v4i wlo = __builtin_amdgcn_raw_buffer_load_b128(wsrs, o0 * 4, 0, 0);
+    const v4i whi = __builtin_amdgcn_raw_buffer_load_b128(wsrs, o0 * 4 + 16, 0, 0);
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        v[j] = __builtin_fmaf((float)S[j], xs * __int_as_float(wlo[j]), 0.0f);
+        v[4 + j] = __builtin_fmaf((float)S[4 + j], xs * __int_as_float(whi[j]), 0.0f);
+    }
+    float *yrow = a.y + (int64_t)t * a.out;
+    if (a.vec_ok && o0 >= a.r0 && o0 + 8 <= a.r1) {
+        float old[8] = {0, 0, 0, 0, 0, 0, 0, 0}, bia[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (a.ep == VX_EP_ADD_SCALED) {
+            const float4 p = *(const float4 *)(yrow + o0), q = *(const float4 *)(yrow + o0 + 4);
+            old[0] = p.x, old[1] = p.y, old[2] = p.z, old[3] = p.w, old[4] = q.x, old[5] = q.y, old[6] = q.z,
+            old[7] = q.w;
+        }
+        if (a.bias) {
+            const float4 p = *(const float4 *)(a.bias + o0), q = *(const float4 *)(a.bias + o0 + 4);
+            bia[0] = p.x, bia[1] = p.y, bia[2] = p.z, bia[3] = p.w, bia[4] = q.x, bia[5] = q.y, bia[6] = q.z,
+            bia[7] = q.w;
+        }
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            r[j] = ep_apply(a.ep, a.alpha, old[j], v[j]);
+            if (a.bias) r[j] = r[j] + bia[j];
+        }
+        *(float4 *)(yrow + o0) = make_float4(r[0], r[1], r[2], r[3]);
+        *(float4 *)(yrow + o0 + 4) = make_float4(r[4], r[5], r[6], r[7]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int o = o0 + j;
+            if (o < a.r0 || o >= a.r1) continue;
+            float r = ep_apply(a.ep, a.alpha, a.ep == VX_EP_ADD_SCALED ? yrow[o] : 0.0f, v[j]);
+            if (a.bias) r = r + a.bias[o];
+            yrow[o] = r;
+        }
+    }
+    if constexpr (GS) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int o = o0 + j;
+            if (o >= a.r0 && o < a.r1) a.gs[(int64_t)t * a.out + o] = S[j];
+        }
+    }
 }
+
 
 namespace {
 
-struct Tile {
+// Launch geometry: grid.x covers the output rows [n_base, r1) in BN = 64*NT steps, grid.y the tokens
+// [m_base, t1) in BM = 16*MT steps (n_base and m_base are r0 and t0 rounded down to 16).
+template <int MT, int NT>
+dim3 grid_of(const GemmArgs &a) {
+    return dim3((unsigned)((a.r1 - a.n_base + 64 * NT - 1) / (64 * NT)),
+                (unsigned)((a.t1 - a.m_base + 16 * MT - 1) / (16 * MT)));
+}
+
+// Ring depth of the direct kernel: as many stages as fit in 60 outstanding loads (the vmcnt counter holds 63) and
+// about 120 registers, at most 16.
+constexpr int direct_depth(int mt, int nt, bool tern, bool single, int ks) {
+    const int loads = ks * (mt + nt) + (single ? 0 : (tern ? 2 : 1) * mt + nt);
+    const int regs = ks * (4 * mt + (tern ? 1 : 4) * nt) + (single ? 0 : 8 * mt + nt);
+    int d = 60 / loads;
+    if (d * regs > 120) d = 120 / regs;
+    if (d > 16) d = 16;
+    return d < 1 ? 1 : d;
+}
+
+template <int MT, int NT, bool TERN, bool GS>
+void launch_direct(const GemmArgs &a, bool single, hipStream_t st) {
+    const dim3 grid = grid_of<MT, NT>(a);
+    if (single) {
+        constexpr int D = direct_depth(MT, NT, TERN, true, 1);
+        tgemm_direct_kernel<MT, NT, TERN, GS, true, 1, D><<<grid, 256, 0, st>>>(a);
+    } else if (a.spg == 2) {
+        constexpr int D = direct_depth(MT, NT, TERN, false, 2);
+        tgemm_direct_kernel<MT, NT, TERN, GS, false, 2, D><<<grid, 256, 0, st>>>(a);
+    } else {
+        constexpr int D = direct_depth(MT, NT, TERN, false, 1);
+        tgemm_direct_kernel<MT, NT, TERN, GS, false, 1, D><<<grid, 256, 0, st>>>(a);
+    }
+}
+
+template <int MT, int NT, bool TERN, bool GS>
+void launch_lds(const GemmArgs &a, bool single, int d, hipStream_t st) {
+    const dim3 grid = grid_of<MT, NT>(a);
+    if (d == 8) {
+        if (single)
+            tgemm_kernel<MT, NT, TERN, GS, true, 8><<<grid, 256, 0, st>>>(a);
+        else
+            tgemm_kernel<MT, NT, TERN, GS, false, 8><<<grid, 256, 0, st>>>(a);
+    } else {
+        // any group and step count (one stage in flight)
+        tgemm_kernel<MT, NT, TERN, GS, false, 1><<<grid, 256, 0, st>>>(a);
+    }
+}
+
+enum Kind { kDirect, kSplitK, kLds };
+
+struct Plan {
+    Kind kind;
     int mt, nt;
 };
 
-// Largest tile that still gives at least two workgroups per CU (256 CUs); the smallest one otherwise.
-Tile choose_tile(int64_t m, int64_t nrows) {
-    static const Tile tiles[] = {{4, 4}, {4, 2}, {2, 4}, {2, 2}, {1, 2}, {1, 1}};
+int64_t wgs_of(const GemmArgs &a, int bm, int bn) {
+    return ((a.r1 - a.n_base + bn - 1) / bn) * ((a.t1 - a.m_base + bm - 1) / bm);
+}
+
+// Kernel and tile per shape. One group (G = K) with up to 1024 tokens and K a multiple of 256 takes the split-K
+// kernel; the large-token ternary shapes whose K is a multiple of 512 the LDS-staged kernel; everything else the
+// direct kernel (one group, or 64 or 128 columns per group) or, for other group sizes, the LDS-staged kernel with
+// one stage in flight. VX_GEMM=direct|splitk|lds and VX_TILE=MTxNT override (tuning).
+Plan plan_for(const GemmArgs &a, bool tern, bool gs, bool single) {
+    const bool direct_ok = single || a.spg == 1 || a.spg == 2;
+    const bool splitk_ok = single && (a.inp / 64) % 4 == 0;
+    const bool lds_fast_ok = tern && !gs && (a.inp / 64) % 8 == 0;
+    const int64_t m = a.t1 - a.m_base;
+    Kind kind = !direct_ok ? kLds : (splitk_ok && m <= 1024) ? kSplitK : (lds_fast_ok && m > 1024) ? kLds : kDirect;
+    const char *kv = getenv("VX_GEMM");
+    if (kv && *kv) {
+        if (!strcmp(kv, "lds") && lds_fast_ok) kind = kLds;
+        if (!strcmp(kv, "direct") && direct_ok) kind = kDirect;
+        if (!strcmp(kv, "splitk") && splitk_ok) kind = kSplitK;
+    }
+    static const Plan dtiles[] = {{kDirect, 4, 4}, {kDirect, 2, 4}, {kDirect, 2, 2}, {kDirect, 1, 2}, {kDirect, 1, 1}};
+    static const Plan ltiles[] = {{kLds, 4, 4}, {kLds, 4, 2}, {kLds, 2, 4}};
+    static const Plan stiles[] = {{kSplitK, 2, 4}, {kSplitK, 1, 8}, {kSplitK, 4, 2}};
+    const Plan *tiles = kind == kDirect ? dtiles : kind == kLds ? ltiles : stiles;
+    const int ntiles = kind == kDirect ? 5 : 3;
     const char *env = getenv("VX_TILE");
-    if (env && *env) {
-        int mt = 0, nt = 0;
-        if (sscanf(env, "%dx%d", &mt, &nt) == 2)
-            for (const Tile &t : tiles)
-                if (t.mt == mt && t.nt == nt) return t;
+    int emt = 0, ent = 0;
+    if (env && *env && sscanf(env, "%dx%d", &emt, &ent) == 2) {
+        for (int i = 0; i < ntiles; i++)
+            if (tiles[i].mt == emt && tiles[i].nt == ent) return tiles[i];
     }
-    for (const Tile &t : tiles) {
-        int64_t wgs = ((m + 16 * t.mt - 1) / (16 * t.mt)) * ((nrows + 64 * t.nt - 1) / (64 * t.nt));
-        if (wgs >= 512) return t;
-    }
-    return tiles[sizeof(tiles) / sizeof(tiles[0]) - 1];
+    if (kind == kLds) return m >= 4096 ? ltiles[1] : ltiles[2];
+    if (kind == kSplitK) return stiles[0];
+    for (int i = 0; i < ntiles; i++)
+        if (wgs_of(a, 16 * tiles[i].mt, 64 * tiles[i].nt) >= 1024) return tiles[i];
+    return tiles[ntiles - 1];
+}
+
+template <int MT, int NT, bool TERN, bool GS>
+void launch_splitk(const GemmArgs &a, hipStream_t st) {
+    const dim3 grid((unsigned)((a.r1 - a.n_base + 16 * NT - 1) / (16 * NT)),
+                    (unsigned)((a.t1 - a.m_base + 16 * MT - 1) / (16 * MT)));
+    // ring depth: every step of the wave's quarter of K when it fits in about 100 registers, else 8 (or fewer)
+    const int nkw = (int)(a.inp / 64) / 4;
+    constexpr int REGS = 4 * MT + (TERN ? 1 : 4) * NT;
+    constexpr int DMAX = 100 / REGS >= 16 ? 16 : (100 / REGS >= 8 ? 8 : 4);
+    if (DMAX >= 16 && nkw % 16 == 0)
+        tgemm_splitk_kernel<MT, NT, TERN, GS, (DMAX >= 16 ? 16 : 1)><<<grid, 256, 0, st>>>(a);
+    else if (DMAX >= 8 && nkw % 8 == 0)
+        tgemm_splitk_kernel<MT, NT, TERN, GS, (DMAX >= 8 ? 8 : 1)><<<grid, 256, 0, st>>>(a);
+    else if (nkw % 4 == 0)
+        tgemm_splitk_kernel<MT, NT, TERN, GS, 4><<<grid, 256, 0, st>>>(a);
+    else if (nkw % 2 == 0)
+        tgemm_splitk_kernel<MT, NT, TERN, GS, 2><<<grid, 256, 0, st>>>(a);
+    else
+        tgemm_splitk_kernel<MT, NT, TERN, GS, 1><<<grid, 256, 0, st>>>(a);
+}
+
+#define VX_DISPATCH_TERN_GS(FN, ...)                   \
+    do {                                               \
+        if (tern) {                                    \
+            if (gs)                                    \
+                FN<MT, NT, true, true>(__VA_ARGS__);   \
+            else                                       \
+                FN<MT, NT, true, false>(__VA_ARGS__);  \
+        } else {                                       \
+            if (gs)                                    \
+                FN<MT, NT, false, true>(__VA_ARGS__);  \
+            else                                       \
+                FN<MT, NT, false, false>(__VA_ARGS__); \
+        }                                              \
+    } while (0)
+
+template <int MT, int NT>
+void run_splitk(const GemmArgs &a, bool tern, bool gs, hipStream_t st) {
+    VX_DISPATCH_TERN_GS(launch_splitk, a, st);
 }
 
 template <int MT, int NT>
-void launch_tile(const GemmArgs &a, bool tern, bool gs, hipStream_t st) {
-    constexpr int BM = MT * 16, BN = NT * 64;
-    dim3 grid((unsigned)((a.r1 - a.n_base + BN - 1) / BN), (unsigned)((a.t1 - a.t0 + BM - 1) / BM));
-    if (tern) {
-        if (gs)
-            tgemm_kernel<MT, NT, true, true><<<grid, 256, 0, st>>>(a);
-        else
-            tgemm_kernel<MT, NT, true, false><<<grid, 256, 0, st>>>(a);
-    } else {
-        if (gs)
-            tgemm_kernel<MT, NT, false, true><<<grid, 256, 0, st>>>(a);
-        else
-            tgemm_kernel<MT, NT, false, false><<<grid, 256, 0, st>>>(a);
-    }
+void run_direct(const GemmArgs &a, bool tern, bool gs, bool single, hipStream_t st) {
+    VX_DISPATCH_TERN_GS(launch_direct, a, single, st);
+}
+
+template <int MT, int NT>
+void run_lds(const GemmArgs &a, bool tern, bool gs, bool single, int d, hipStream_t st) {
+    VX_DISPATCH_TERN_GS(launch_lds, a, single, d, st);
 }
 
 }  // namespace
 
-void gemm(const TMat *w, const int8_t *xq, const float *xs, const int32_t *xg, int64_t n, float *y,
+void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y,
           const float *bias, int ep, float alpha, int32_t *gs, int64_t r0, int64_t r1, int64_t t0, int64_t t1,
           hipStream_t st) {
     require(w != nullptr, "weight matrix must not be NULL");
-    require(xq && xs && y, "xq, xs and y must not be NULL");
-    require(!w->ternary || xg, "ternary weights need the activation code sums (xgsum)");
+    require(xq && xs_t && y, "xq, xs_t and y must not be NULL");
+    require(!w->ternary || xg_t, "ternary weights need the activation code sums (xgsum_t)");
     require(ep == VX_EP_STORE || ep == VX_EP_SILU || ep == VX_EP_ADD_SCALED, "unknown epilogue");
     require(n >= 0, "n must be >= 0");
     require(0 <= r0 && r0 <= r1 && r1 <= w->out, "row range outside [0, out]");
     require(0 <= t0 && t0 <= t1 && t1 <= n, "token range outside [0, n]");
-    require((n + 256) * w->inp < (1ll << 32) && n * w->ng * 4 < (1ll << 32), "activation operand above 4 GiB");
+    const int64_t np = (n + 15) / 16 * 16;
+    require((np + 256) * w->inp < (1ll << 31) && np * w->ng * 4 < (1ll << 31), "activation operand above 2 GiB");
     if (r0 == r1 || t0 == t1) return;
     GemmArgs a;
     a.w = w->wdev;
     a.ws_t = w->scales_t;
     a.xq = xq;
-    a.xs = xs;
-    a.xg = xg;
+    a.xs = xs_t;
+    a.xg = xg_t;
     a.y = y;
     a.bias = bias;
     a.gs = gs;
     a.n = n;
+    a.np = np;
     a.out = w->out;
     a.inp = w->inp;
     a.ng = w->ng;
@@ -309,29 +863,47 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs, const int32_t *xg, i
     a.t0 = t0;
     a.t1 = t1;
     a.n_base = r0 / 16 * 16;
+    a.m_base = t0 / 16 * 16;
     const int64_t wbytes = (w->out_pad / 16) * (w->inp / 64) * 64 * (w->ternary ? 4 : 16);
-    require(wbytes < (1ll << 32), "weight plane above 4 GiB");
+    require(wbytes < (1ll << 31), "weight plane above 2 GiB");
     a.w_bytes = (uint32_t)wbytes;
     a.ws_bytes = (uint32_t)(w->ng * w->out_pad * 4);
     a.xq_bytes = (uint32_t)(n * w->inp);
-    a.xs_bytes = (uint32_t)(n * w->ng * 4);
+    a.xs_bytes = (uint32_t)(w->ng * np * 4);
     a.ep = ep;
     a.alpha = alpha;
-    const Tile t = choose_tile(t1 - t0, r1 - a.n_base);
-    const bool tern = w->ternary, g = gs != nullptr;
-    if (t.mt == 4 && t.nt == 4)
-        launch_tile<4, 4>(a, tern, g, st);
-    else if (t.mt == 4 && t.nt == 2)
-        launch_tile<4, 2>(a, tern, g, st);
-    else if (t.mt == 2 && t.nt == 4)
-        launch_tile<2, 4>(a, tern, g, st);
-    else if (t.mt == 2 && t.nt == 2)
-        launch_tile<2, 2>(a, tern, g, st);
-    else if (t.mt == 1 && t.nt == 2)
-        launch_tile<1, 2>(a, tern, g, st);
-    else
-        launch_tile<1, 1>(a, tern, g, st);
-    hip_check(hipGetLastError(), "tgemm_kernel launch");
+    const bool tern = w->ternary, g = gs != nullptr, single = w->ng == 1;
+    a.vec_ok = (w->out % 4 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
+               (!bias || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
+    const Plan p = plan_for(a, tern, g, single);
+    if (p.kind == kSplitK) {
+        if (p.mt == 2 && p.nt == 4)
+            run_splitk<2, 4>(a, tern, g, st);
+        else if (p.mt == 1 && p.nt == 8)
+            run_splitk<1, 8>(a, tern, g, st);
+        else
+            run_splitk<4, 2>(a, tern, g, st);
+    } else if (p.kind == kDirect) {
+        if (p.mt == 4 && p.nt == 4)
+            run_direct<4, 4>(a, tern, g, single, st);
+        else if (p.mt == 2 && p.nt == 4)
+            run_direct<2, 4>(a, tern, g, single, st);
+        else if (p.mt == 2 && p.nt == 2)
+            run_direct<2, 2>(a, tern, g, single, st);
+        else if (p.mt == 1 && p.nt == 2)
+            run_direct<1, 2>(a, tern, g, single, st);
+        else
+            run_direct<1, 1>(a, tern, g, single, st);
+    } else {
+        const int d = (tern && !g && (a.inp / 64) % 8 == 0) ? 8 : 1;
+        if (p.mt == 4 && p.nt == 4)
+            run_lds<4, 4>(a, tern, g, single, d, st);
+        else if (p.mt == 4 && p.nt == 2)
+            run_lds<4, 2>(a, tern, g, single, d, st);
+        else
+            run_lds<2, 4>(a, tern, g, single, d, st);
+    }
+    hip_check(hipGetLastError(), "tgemm launch");
 }
 
 }  // namespace vx

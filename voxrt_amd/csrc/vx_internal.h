@@ -17,8 +17,10 @@ namespace vx {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // Device weight matrix. Ternary matrices hold 2-bit codes (trit + 1) in the MFMA operand order; int8 matrices
-// hold the bytes themselves in the same block order. Rows are padded to a multiple of kRowPad with zero weights
-// and zero scales, so every workgroup column tile reads inside the allocation.
+// hold the bytes themselves in the same block order. Rows are padded with zero weights and zero scales to a
+// multiple of kRowPad plus one more kRowPad, so every workgroup column tile (at most kRowPad rows, starting at or
+// below the last real row) reads inside the allocation even when its row offset travels in a scalar register,
+// which the buffer range check does not cover.
 constexpr int kRowPad = 256;
 
 struct TMat {
@@ -53,6 +55,9 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes
 }
 
 __device__ inline float bits_f32(uint32_t u) { return __uint_as_float(u); }
+
+// Note: reinterpret an element of an ext_vector_type through __int_as_float(v[e]), never
+// __builtin_bit_cast(float, v[e]): this clang lowers the latter to element 0 whatever e is.
 
 // exp_poly (crates/voxrt/src/tensor.rs:829-848): clamp to [-87, 88], n = rint(x * log2 e), two fma reduction
 // steps, degree-6 Horner by fma, times 2^n. Each step is one IEEE operation (the library is built with

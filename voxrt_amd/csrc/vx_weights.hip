@@ -121,7 +121,7 @@ vx_tmat *new_tmat(int64_t out, int64_t inp, int64_t group, bool ternary) {
     m->inp = inp;
     m->group = group;
     m->ng = inp / group;
-    m->out_pad = (out + kRowPad - 1) / kRowPad * kRowPad;
+    m->out_pad = (out + kRowPad - 1) / kRowPad * kRowPad + kRowPad;
     m->ternary = ternary;
     return h;
 }

@@ -191,13 +191,29 @@ class TernaryMatrix:
             pass
 
 
-class QuantAct:
-    """Quantised activations on the device (packed.rs:286-298): codes int8 [n, inp], scales float32 [n, ng] and
-    the per-(token, group) code sums gsum int32 [n, ng]."""
+def npad(n: int) -> int:
+    """Padded token count of the transposed activation tables (VX_NPAD)."""
+    return (n + 15) // 16 * 16
 
-    def __init__(self, q, scales, gsum, n: int, inp: int, group: int):
-        self.x, self.scales, self.gsum = q, scales, gsum
+
+class QuantAct:
+    """Quantised activations on the device (packed.rs:286-298): codes int8 [n, inp], and the per-(token, group)
+    scales and code sums transposed, scales_t float32 [ng, npad(n)] and gsum_t int32 [ng, npad(n)]
+    (QuantAct::scales_t, packed.rs:294; pad tokens zero)."""
+
+    def __init__(self, q, scales_t, gsum_t, n: int, inp: int, group: int):
+        self.x, self.scales_t, self.gsum_t = q, scales_t, gsum_t
         self.n, self.inp, self.group = n, inp, group
+
+    @property
+    def scales(self):
+        """[n, ng] view of the scales (QuantAct::scales)."""
+        return self.scales_t[:, : self.n].t()
+
+    @property
+    def gsum(self):
+        """[n, ng] view of the code sums (QuantAct::gsum)."""
+        return self.gsum_t[:, : self.n].t()
 
     @classmethod
     def quantize(cls, x, group: int, stream=None) -> "QuantAct":
@@ -208,10 +224,10 @@ class QuantAct:
         if group <= 0 or inp % group:
             raise ValueError("inp must be a multiple of group")
         q = torch.empty((n, inp), dtype=torch.int8, device=x.device)
-        s = torch.empty((n, inp // group), dtype=torch.float32, device=x.device)
-        g = torch.empty((n, inp // group), dtype=torch.int32, device=x.device)
+        s = torch.empty((inp // group, npad(n)), dtype=torch.float32, device=x.device)
+        g = torch.empty((inp // group, npad(n)), dtype=torch.int32, device=x.device)
         check(lib().vx_quantize(_dev_ptr(x, torch.float32, "x"), n, inp, group, _dev_ptr(q, torch.int8, "q"),
-                                _dev_ptr(s, torch.float32, "scales"), _dev_ptr(g, torch.int32, "gsum"),
+                                _dev_ptr(s, torch.float32, "scales_t"), _dev_ptr(g, torch.int32, "gsum_t"),
                                 _stream(stream)))
         return cls(q, s, g, n, inp, group)
 
@@ -226,8 +242,8 @@ def gemm_ep(w: TernaryMatrix, x: QuantAct, y, bias=None, ep: Epilogue = Epilogue
         raise ValueError("activation and weight shapes or groups differ")
     if tuple(y.shape) != (x.n, w.out):
         raise ValueError("y must be [n, out]")
-    check(lib().vx_gemm_ep(w._h, _dev_ptr(x.x, torch.int8, "x"), _dev_ptr(x.scales, torch.float32, "scales"),
-                           _dev_ptr(x.gsum, torch.int32, "gsum"), x.n, _dev_ptr(y, torch.float32, "y"),
+    check(lib().vx_gemm_ep(w._h, _dev_ptr(x.x, torch.int8, "x"), _dev_ptr(x.scales_t, torch.float32, "scales_t"),
+                           _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), x.n, _dev_ptr(y, torch.float32, "y"),
                            _dev_ptr(bias, torch.float32, "bias"), ep.kind, ep.alpha,
                            _dev_ptr(group_sums, torch.int32, "group_sums"), _stream(stream)))
 
@@ -243,6 +259,7 @@ def gemm_rows_range(w: TernaryMatrix, x: QuantAct, y, r0: int, r1: int, t0: int,
 
     if x.inp != w.inp or x.group != w.group:
         raise ValueError("activation and weight shapes or groups differ")
-    check(lib().vx_gemm_rows_range(w._h, _dev_ptr(x.x, torch.int8, "x"), _dev_ptr(x.scales, torch.float32, "scales"),
-                                   _dev_ptr(x.gsum, torch.int32, "gsum"), x.n, _dev_ptr(y, torch.float32, "y"), r0,
+    check(lib().vx_gemm_rows_range(w._h, _dev_ptr(x.x, torch.int8, "x"),
+                                   _dev_ptr(x.scales_t, torch.float32, "scales_t"),
+                                   _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), x.n, _dev_ptr(y, torch.float32, "y"), r0,
                                    r1, t0, t1, ep.kind, ep.alpha, _stream(stream)))
