@@ -315,16 +315,71 @@ def test_ffn_up_t338_bit_exact(dev, orc, group):
 
 
 @pytest.mark.parametrize("k,n_out", [(1024, 4096), (4096, 1024)])
-def test_batched_m8192_sampled_rows(dev, orc, k, n_out):
-    """M=8192 (the batched regime): 96 sampled tokens and every output row against the oracle, bit-exact."""
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_batched_m8192_sampled_rows(dev, orc, k, n_out, per_channel):
+    """M=8192 (the batched regime): 96 sampled tokens and every output row against the oracle, bit-exact; G=128
+    (f16 scales) and per-channel G=K (fp32 scales, the large-token kernel)."""
     import voxrt_amd as vx
 
     m = 8192
-    trits, s16, x = _workload(orc, m, k, n_out, 128, seed_cfg=2)
-    w = vx.TernaryMatrix.from_packed(synth.pack_rows(trits), s16, n_out, k, 128)
-    _, got, _ = _device_gemm(vx, dev, w, x, 128)
+    group = k if per_channel else 128
+    trits, s16, x = _workload(orc, m, k, n_out, group, seed_cfg=2)
+    ws = orc.f16_to_f32(s16)
+    qw = synth.pack_rows(trits)
+    w = vx.TernaryMatrix.from_packed_f32(qw, ws, n_out, k, group) if per_channel else \
+        vx.TernaryMatrix.from_packed(qw, s16, n_out, k, group)
+    _, got, _ = _device_gemm(vx, dev, w, x, group)
     pick = np.sort(np.random.default_rng(0).choice(m, 96, replace=False))
     pick[-1] = m - 1
-    q, xs, _ = orc.quantize(x[pick], 128)
-    want = orc.gemm(trits, orc.f16_to_f32(s16), q, xs, 128)
-    _assert_bits_equal(got[pick], want, f"M=8192 K={k} N={n_out} sampled")
+    q, xs, _ = orc.quantize(x[pick], group)
+    want = orc.gemm(trits, ws, q, xs, group)
+    _assert_bits_equal(got[pick], want, f"M=8192 K={k} N={n_out} G={group} sampled")
+
+
+@pytest.mark.parametrize("m,k,n_out", [(1300, 512, 300), (2048, 1024, 512)])
+def test_large_token_kernel_epilogues_and_bias(dev, orc, m, k, n_out):
+    """More than 1024 tokens with one group (G = K) takes the large-token kernel: ragged tiles (1300 x 300) and
+    whole tiles (2048 x 512), each epilogue with and without bias, bit-exact against the oracle."""
+    import torch
+
+    import voxrt_amd as vx
+
+    trits, s16, x = _workload(orc, m, k, n_out, k, seed_cfg=3)
+    ws = orc.f16_to_f32(s16)
+    w = vx.TernaryMatrix.from_packed_f32(synth.pack_rows(trits), ws, n_out, k, k)
+    q, xs, _ = orc.quantize(x, k)
+    xa = vx.QuantAct.quantize(_t(x, dev), k)
+    rng = synth.Lcg(31)
+    base = ((rng.take(m * n_out) % 200).astype(np.float32) * np.float32(0.01) - np.float32(1.0)).reshape(m, n_out)
+    bias = (rng.take(n_out) % 100).astype(np.float32) / np.float32(10.0)
+    for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
+        want = orc.gemm(trits, ws, q, xs, k, y=base.copy(), ep=ep_kind, alpha=alpha)
+        for with_bias in (False, True):
+            y = _t(base, dev)
+            vx.gemm_ep(w, xa, y, _t(bias, dev) if with_bias else None, _ep_of(vx, ep_kind, alpha))
+            exp = (want + bias[None, :]).astype(np.float32) if with_bias else want
+            _assert_bits_equal(y.cpu().numpy(), exp, f"{m}x{k}x{n_out} ep={ep_kind} bias={with_bias}")
+
+
+def test_large_token_kernel_ranges_with_nan_canary(dev, orc):
+    """Row and token windows on the large-token kernel: every element inside equals the oracle and nothing
+    outside is written (a NaN canary), including windows that start and end inside a tile."""
+    import torch
+
+    import voxrt_amd as vx
+
+    m, k, n_out = 1500, 512, 600
+    trits, s16, x = _workload(orc, m, k, n_out, k, seed_cfg=4)
+    ws = orc.f16_to_f32(s16)
+    w = vx.TernaryMatrix.from_packed_f32(synth.pack_rows(trits), ws, n_out, k, k)
+    q, xs, _ = orc.quantize(x, k)
+    want = orc.gemm(trits, ws, q, xs, k)
+    xa = vx.QuantAct.quantize(_t(x, dev), k)
+    for r0, r1, t0, t1 in [(0, n_out, 0, m), (5, 590, 3, 1497), (256, 512, 0, 1300), (17, 300, 200, 1400)]:
+        y = torch.full((m, n_out), float("nan"), dtype=torch.float32, device=dev)
+        vx.gemm_rows_range(w, xa, y, r0, r1, t0, t1)
+        got = y.cpu().numpy()
+        inside = np.zeros((m, n_out), bool)
+        inside[t0:t1, r0:r1] = True
+        assert (np.isnan(got) == ~inside).all(), f"stray write rows {r0}..{r1} toks {t0}..{t1}"
+        _assert_bits_equal(got[inside], want[inside], f"rows {r0}..{r1} toks {t0}..{t1}")

@@ -43,7 +43,7 @@ struct GemmArgs {
     int32_t *gs;            // [ng][n][out] or NULL
     int64_t n, np, out, inp, ng, out_pad, spg;
     int64_t r0, r1, t0, t1, n_base, m_base;
-    uint32_t w_bytes, ws_bytes, xq_bytes, xs_bytes;
+    uint32_t w_bytes, ws_bytes, xq_bytes, xs_bytes, y_bytes;
     int ep;
     float alpha;
     int vec_ok;  // y (and bias) rows are 16-byte aligned: out % 4 == 0 and 16-byte aligned base pointers
@@ -682,6 +682,234 @@ __global__ __launch_bounds__(256) void tgemm_splitk_kernel(const GemmArgs a) {
 }
 
 
+// ---------------------------------------------------------------------------------------------------------------
+// Large-token kernel (one group, G = K; K a multiple of 512). Built for MFMA throughput:
+//  * v_mfma_i32_32x32x32_i8: a wavefront owns a 128 x 64 output tile (4 x 2 blocks of 32 x 32, 128 int32
+//    accumulators); D element v of lane l is row (v/4)*8 + (l/32)*4 + v%4, column l%32 of its block.
+//  * the workgroup's 128 x 64 activation tile of each K step reaches LDS by buffer_load ... lds (no registers),
+//    in MFMA-fragment order: fragment f = 4*khalf + rowblock is 1 KB, lane l's 16 bytes at l*16, so every
+//    ds_read_b128 is linear. Four LDS slots: steps kb+1 .. kb+3 are in flight while kb computes, and the
+//    fragments of kb+1 are read while the MFMAs of kb run.
+//  * each wavefront gathers its weight codes (one dword per lane per 32 x 32 block half) from the 16-row block
+//    layout into a 4-deep register ring; all per-step offsets are scalar.
+//  * one explicit vmcnt wait and one barrier per step; the loads of a step are issued in a fixed order, so the
+//    wait count is a constant (10: the B loads of step kb-2+4 and the 6 loads of step kb-1 may be pending).
+//  * the accumulators start at -sum(x codes) of their token, so they end at S; the fold fma(S, xs * ws, 0) and
+//    the epilogue are specialised on the epilogue kind and the bias, with buffer stores for whole tiles.
+template <int EP, bool BIAS>
+__global__ __launch_bounds__(256, 2) void tgemm_big_kernel(const GemmArgs a) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    __shared__ __attribute__((aligned(1024))) int8_t sa0[8192];
+    __shared__ __attribute__((aligned(1024))) int8_t sa1[8192];
+    __shared__ __attribute__((aligned(1024))) int8_t sa2[8192];
+    __shared__ __attribute__((aligned(1024))) int8_t sa3[8192];
+    auto slot = [&](int i) -> int8_t * { return i == 0 ? sa0 : i == 1 ? sa1 : i == 2 ? sa2 : sa3; };
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, lh = lane >> 5;
+    const int m0 = (int)a.m_base + (int)blockIdx.y * 128;
+    const int nw0 = (int)a.n_base + (int)blockIdx.x * 256 + wave * 64;
+    const int inp = (int)a.inp, nk = inp / 64;
+    constexpr uint32_t kOff = 0xFFFFFFF0u;
+
+    const auto xrs = make_rsrc(a.xq, a.xq_bytes);
+    const auto wrs = make_rsrc(a.w, a.w_bytes);
+
+    // activation DMA: this wave moves fragments f = 2*wave and 2*wave+1 of every step
+    uint32_t vdma[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int f = 2 * wave + q, kh = f >> 2, rb = f & 3;
+        vdma[q] = (uint32_t)((m0 + rb * 32 + l32) * inp + kh * 32 + 16 * lh);
+    }
+    // weight gather: block half (cb, kh) of lane l = row nw0 + 32cb + l%32, columns 32kh + 16*(l/32) .. +15,
+    // i.e. 16-row block (nw0 + 32cb)/16 + (l%32)/16, lane' = 16*(2kh + l/32) + l%16 of the 16x64 layout
+    constexpr int BB = 4;  // bytes of weight codes per lane per 16 x 64 block
+    uint32_t vb[2][2];
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) {
+            const int nb16 = (nw0 + 32 * cb) / 16 + (l32 >> 4);
+            vb[cb][kh] = (uint32_t)((nb16 * nk * 64 + 16 * (2 * kh + lh) + (lane & 15)) * BB);
+        }
+
+    uint32_t rb[4][2][2];
+    // `live` is a compile-time constant at every call: loads past the last step keep the issue order (and so
+    // the constant wait count) with an out-of-range offset, which reads zeros and touches no memory
+    auto dma = [&](int kb, int sl, bool live) {
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(slot(sl) + (2 * wave + q) * 1024), 16,
+                                                     live ? vdma[q] : kOff, kb * 64, 0, 0);
+    };
+    auto bload = [&](int kb, int ring, bool live) {
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++)
+                rb[ring][cb][kh] = __builtin_amdgcn_raw_buffer_load_b32(wrs, live ? vb[cb][kh] : kOff, kb * 64 * BB, 0);
+    };
+    // fragments of one step: [khalf][rowblock]
+    v4i fr[2][2][4];
+    auto read_frags = [&](int sl, int set) {
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) fr[set][kh][r] = *(const v4i *)(slot(sl) + (kh * 4 + r) * 1024 + lane * 16);
+    };
+    // accumulators seeded with -sum(x codes) of their token (codes are trit + 1), so they end at S
+    typedef int v16i __attribute__((ext_vector_type(16)));
+    v16i acc[4][2];
+    {
+        const auto grs = make_rsrc(a.xg, a.xs_bytes);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int vq = 0; vq < 4; vq++) {
+                const v4i g4 = __builtin_amdgcn_raw_buffer_load_b128(grs, (uint32_t)((m0 + r * 32 + vq * 8 + lh * 4) * 4), 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[r][0][vq * 4 + e] = acc[r][1][vq * 4 + e] = -g4[e];
+            }
+    }
+
+    // Per wave the loads are issued as  bload(0) dma(0) bload(1) dma(1) ... dma(j) bload(j+1) ...; at the top of
+    // step kb the activation DMA of step kb+1 is complete once at most bload(kb+2), dma(kb+2), bload(kb+3) (10
+    // loads) are outstanding.
+    constexpr int kWait = 10 | (7 << 4) | (15 << 8);  // vmcnt(10); expcnt, lgkmcnt not waited
+    constexpr int kWait0 = 16 | (7 << 4) | (15 << 8);  // vmcnt(16): dma(0) complete in the prologue
+    auto step = [&](int kb, int i, bool dma_live, bool b_live, bool next) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kWait);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        dma(kb + 3, (i + 3) & 3, dma_live);
+        if (next) read_frags((i + 1) & 3, (i + 1) & 1);
+        // keep the fragment reads of step kb+1 ahead of the MFMAs of step kb (two fragment sets live)
+        __builtin_amdgcn_sched_barrier(0);
+        v4i bv[2][2];
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++) bv[cb][kh] = widen_codes(rb[i][cb][kh]);
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int cb = 0; cb < 2; cb++)
+                    acc[r][cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[i & 1][kh][r], bv[cb][kh], acc[r][cb], 0, 0,
+                                                                        0);
+        __builtin_amdgcn_sched_barrier(0);
+        bload(kb + 4, i, b_live);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    bload(0, 0, true);
+    dma(0, 0, true);
+    bload(1, 1, true);
+    dma(1, 1, true);
+    bload(2, 2, true);
+    dma(2, 2, true);
+    bload(3, 3, true);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWait0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(0, 0);
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0 << 8) | 0x3f);  // lgkmcnt(0): nothing of the prologue left
+    __builtin_amdgcn_sched_barrier(0);
+
+    // nk is a multiple of 8: all steps but the last four load steps kb+3 and kb+4
+    for (int kb0 = 0; kb0 < nk - 4; kb0 += 4) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) step(kb0 + i, i, true, true, true);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) step(nk - 4 + i, i, i == 0, false, i < 3);
+    __builtin_amdgcn_s_waitcnt(0);
+
+    // epilogue: the accumulators hold S (seeded with -gsum), y = ep(fma((float)S, xs * ws, 0)) (+ bias)
+    const auto srs = make_rsrc(a.xs, a.xs_bytes);
+    const auto wsrs = make_rsrc(a.ws_t, a.ws_bytes);
+    float wsv[2], bia[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++) {
+        const int o = nw0 + cb * 32 + l32;
+        wsv[cb] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wsrs, (uint32_t)(o * 4), 0, 0));
+        if constexpr (BIAS) bia[cb] = (o >= a.r0 && o < a.r1) ? a.bias[o] : 0.0f;
+    }
+    const bool full = m0 >= a.t0 && m0 + 128 <= a.t1 && nw0 >= a.r0 && nw0 + 64 <= a.r1;
+    if (full) {
+        // whole wave tile inside the window: buffer stores, the row offset in a scalar register
+        const auto yrs = make_rsrc(a.y, a.y_bytes);
+        const uint32_t out4 = (uint32_t)a.out * 4;
+        const uint32_t vy = (uint32_t)(lh * 4) * out4 + (uint32_t)(nw0 + l32) * 4;
+        v4i xs4a[4][4];  // all 16 token-scale quads in one batch (the fragment registers are free by now)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int vq = 0; vq < 4; vq++)
+                xs4a[r][vq] = __builtin_amdgcn_raw_buffer_load_b128(
+                    srs, (uint32_t)((m0 + r * 32 + vq * 8 + lh * 4) * 4), 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int vq = 0; vq < 4; vq++) {
+                const v4i xs4 = xs4a[r][vq];
+                float old[4][2];
+                if constexpr (EP == VX_EP_ADD_SCALED) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+#pragma unroll
+                        for (int cb = 0; cb < 2; cb++)
+                            old[e][cb] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                                yrs, vy + cb * 128, (uint32_t)(m0 + r * 32 + vq * 8 + e) * out4, 0));
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float xsv = __int_as_float(xs4[e]);
+                    const uint32_t so = (uint32_t)(m0 + r * 32 + vq * 8 + e) * out4;
+#pragma unroll
+                    for (int cb = 0; cb < 2; cb++) {
+                        const float v = __builtin_fmaf((float)acc[r][cb][vq * 4 + e], xsv * wsv[cb], 0.0f);
+                        float res = v;
+                        if constexpr (EP == VX_EP_SILU) res = silu_fast(v);
+                        if constexpr (EP == VX_EP_ADD_SCALED) res = __builtin_fmaf(a.alpha, v, old[e][cb]);
+                        if constexpr (BIAS) res = res + bia[cb];
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(res), yrs, vy + cb * 128, so, 0);
+                    }
+                }
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int vq = 0; vq < 4; vq++) {
+                const int t4 = m0 + r * 32 + vq * 8 + lh * 4;
+                const v4i xs4 = __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)(t4 * 4), 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int64_t t = t4 + e;
+                    if (t < a.t0 || t >= a.t1) continue;
+                    const float xsv = __int_as_float(xs4[e]);
+#pragma unroll
+                    for (int cb = 0; cb < 2; cb++) {
+                        const int64_t o = nw0 + cb * 32 + l32;
+                        if (o < a.r0 || o >= a.r1) continue;
+                        const float v = __builtin_fmaf((float)acc[r][cb][vq * 4 + e], xsv * wsv[cb], 0.0f);
+                        float *py = a.y + t * a.out + o;
+                        float res = v;
+                        if constexpr (EP == VX_EP_SILU) res = silu_fast(v);
+                        if constexpr (EP == VX_EP_ADD_SCALED) res = __builtin_fmaf(a.alpha, v, *py);
+                        if constexpr (BIAS) res = res + bia[cb];
+                        *py = res;
+                    }
+                }
+            }
+    }
+}
+
 namespace {
 
 // Launch geometry: grid.x covers the output rows [n_base, r1) in BN = 64*NT steps, grid.y the tokens
@@ -732,7 +960,7 @@ void launch_lds(const GemmArgs &a, bool single, int d, hipStream_t st) {
     }
 }
 
-enum Kind { kDirect, kSplitK, kLds };
+enum Kind { kDirect, kSplitK, kLds, kBig };
 
 struct Plan {
     Kind kind;
@@ -751,14 +979,21 @@ Plan plan_for(const GemmArgs &a, bool tern, bool gs, bool single) {
     const bool direct_ok = single || a.spg == 1 || a.spg == 2;
     const bool splitk_ok = single && (a.inp / 64) % 4 == 0;
     const bool lds_fast_ok = tern && !gs && (a.inp / 64) % 8 == 0;
+    const bool big_ok = tern && single && !gs && (a.inp / 64) % 8 == 0 && a.y_bytes != 0;
     const int64_t m = a.t1 - a.m_base;
-    Kind kind = !direct_ok ? kLds : (splitk_ok && m <= 1024) ? kSplitK : (lds_fast_ok && m > 1024) ? kLds : kDirect;
+    Kind kind = !direct_ok ? kLds
+                : (splitk_ok && m <= 1024) ? kSplitK
+                : (big_ok && m > 1024)     ? kBig
+                : (lds_fast_ok && m > 1024) ? kLds
+                                            : kDirect;
     const char *kv = getenv("VX_GEMM");
     if (kv && *kv) {
         if (!strcmp(kv, "lds") && lds_fast_ok) kind = kLds;
         if (!strcmp(kv, "direct") && direct_ok) kind = kDirect;
         if (!strcmp(kv, "splitk") && splitk_ok) kind = kSplitK;
+        if (!strcmp(kv, "big") && big_ok) kind = kBig;
     }
+    if (kind == kBig) return Plan{kBig, 8, 4};
     static const Plan dtiles[] = {{kDirect, 4, 4}, {kDirect, 2, 4}, {kDirect, 2, 2}, {kDirect, 1, 2}, {kDirect, 1, 1}};
     static const Plan ltiles[] = {{kLds, 4, 4}, {kLds, 4, 2}, {kLds, 2, 4}};
     static const Plan stiles[] = {{kSplitK, 2, 4}, {kSplitK, 1, 8}, {kSplitK, 4, 2}};
@@ -870,13 +1105,21 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
     a.ws_bytes = (uint32_t)(w->ng * w->out_pad * 4);
     a.xq_bytes = (uint32_t)(n * w->inp);
     a.xs_bytes = (uint32_t)(w->ng * np * 4);
+    a.y_bytes = n * w->out * 4 < (1ll << 31) ? (uint32_t)(n * w->out * 4) : 0u;  // 0: no buffer stores
     a.ep = ep;
     a.alpha = alpha;
     const bool tern = w->ternary, g = gs != nullptr, single = w->ng == 1;
     a.vec_ok = (w->out % 4 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
                (!bias || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
     const Plan p = plan_for(a, tern, g, single);
-    if (p.kind == kSplitK) {
+    if (p.kind == kBig) {
+        const dim3 grid((unsigned)((a.r1 - a.n_base + 255) / 256), (unsigned)((a.t1 - a.m_base + 127) / 128));
+        auto k = a.ep == VX_EP_SILU ? (a.bias ? tgemm_big_kernel<VX_EP_SILU, true> : tgemm_big_kernel<VX_EP_SILU, false>)
+                 : a.ep == VX_EP_ADD_SCALED
+                     ? (a.bias ? tgemm_big_kernel<VX_EP_ADD_SCALED, true> : tgemm_big_kernel<VX_EP_ADD_SCALED, false>)
+                     : (a.bias ? tgemm_big_kernel<VX_EP_STORE, true> : tgemm_big_kernel<VX_EP_STORE, false>);
+        k<<<grid, 256, 0, st>>>(a);
+    } else if (p.kind == kSplitK) {
         if (p.mt == 2 && p.nt == 4)
             run_splitk<2, 4>(a, tern, g, st);
         else if (p.mt == 1 && p.nt == 8)
