@@ -687,8 +687,8 @@ __global__ __launch_bounds__(256) void tgemm_splitk_kernel(const GemmArgs a) {
 //  * v_mfma_i32_32x32x32_i8: a wavefront owns a 128 x 64 output tile (4 x 2 blocks of 32 x 32, 128 int32
 //    accumulators); D element v of lane l is row (v/4)*8 + (l/32)*4 + v%4, column l%32 of its block.
 //  * the workgroup's 128 x 64 activation tile of each K step reaches LDS by buffer_load ... lds (no registers),
-//    in MFMA-fragment order: fragment f = 4*khalf + rowblock is 1 KB, lane l's 16 bytes at l*16, so every
-//    ds_read_b128 is linear. Four LDS slots: steps kb+1 .. kb+3 are in flight while kb computes, and the
+//    16 rows x 64 contiguous bytes per instruction, in a chunk-swizzled row layout that keeps the fragment reads
+//    free of bank conflicts. Four LDS slots: steps kb+1 .. kb+3 are in flight while kb computes, and the
 //    fragments of kb+1 are read while the MFMAs of kb run.
 //  * each wavefront gathers its weight codes (one dword per lane per 32 x 32 block half) from the 16-row block
 //    layout into a 4-deep register ring; all per-step offsets are scalar.
@@ -715,12 +715,23 @@ __global__ __launch_bounds__(256, 2) void tgemm_big_kernel(const GemmArgs a) {
     const auto xrs = make_rsrc(a.xq, a.xq_bytes);
     const auto wrs = make_rsrc(a.w, a.w_bytes);
 
-    // activation DMA: this wave moves fragments f = 2*wave and 2*wave+1 of every step
+    // Activation tile of a step in LDS: 8 blocks of 16 token rows x 64 bytes; row i of a block holds its four
+    // 16-byte chunks c at position c ^ swz(i), swz(i) = ((i >> 1) ^ (i >> 2)) & 3, so that the fragment reads
+    // below (32 rows, one chunk each) hit distinct banks for every 8 (and every 16) consecutive lanes. One DMA
+    // instruction fills one block (lane l -> row l/4, position l%4), i.e. 16 rows x 64 contiguous bytes: this wave
+    // moves blocks 2*wave and 2*wave+1.
     uint32_t vdma[2];
+    {
+        const int i = lane >> 2, c = (lane & 3) ^ (((i >> 1) ^ (i >> 2)) & 3);
 #pragma unroll
-    for (int q = 0; q < 2; q++) {
-        const int f = 2 * wave + q, kh = f >> 2, rb = f & 3;
-        vdma[q] = (uint32_t)((m0 + rb * 32 + l32) * inp + kh * 32 + 16 * lh);
+        for (int q = 0; q < 2; q++) vdma[q] = (uint32_t)((m0 + (2 * wave + q) * 16 + i) * inp + c * 16);
+    }
+    // fragment reads: lane l takes row 32*rb + l%32 (block 2*rb + (l%32)/16, row l%16), chunk 2*kh + l/32
+    uint32_t vfr[2];
+    {
+        const int i = lane & 15, sw = ((i >> 1) ^ (i >> 2)) & 3;
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) vfr[kh] = (uint32_t)((l32 >> 4) * 1024 + i * 64 + 16 * ((2 * kh + lh) ^ sw));
     }
     // weight gather: block half (cb, kh) of lane l = row nw0 + 32cb + l%32, columns 32kh + 16*(l/32) .. +15,
     // i.e. 16-row block (nw0 + 32cb)/16 + (l%32)/16, lane' = 16*(2kh + l/32) + l%16 of the 16x64 layout
@@ -756,7 +767,7 @@ __global__ __launch_bounds__(256, 2) void tgemm_big_kernel(const GemmArgs a) {
 #pragma unroll
         for (int kh = 0; kh < 2; kh++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) fr[set][kh][r] = *(const v4i *)(slot(sl) + (kh * 4 + r) * 1024 + lane * 16);
+            for (int r = 0; r < 4; r++) fr[set][kh][r] = *(const v4i *)(slot(sl) + vfr[kh] + r * 2048);
     };
     // accumulators seeded with -sum(x codes) of their token (codes are trit + 1), so they end at S
     typedef int v16i __attribute__((ext_vector_type(16)));
