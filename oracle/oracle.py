@@ -52,6 +52,19 @@ def lib() -> C.CDLL:
             "or_quad16_pack": (None, [P, S, S, S, P, P, P]),
             "or_gemm_vnni_range": (None, [P, P, S, S, S, P, P, P, S, P, S, S, S, S, I, F]),
             "or_gemm_ep_vnni": (None, [P, P, S, S, S, P, P, P, S, P, I, F, I, S]),
+            "or_row_mean_var": (None, [P, S, P, P]),
+            "or_layer_norm": (None, [P, S, S, P, P, P]),
+            "or_quantize_normed": (None, [P, S, S, S, P, P, P, P, P]),
+            "or_exp_row_scaled": (F, [P, S, F]),
+            "or_glu": (None, [P, S, S, P]),
+            "or_fold_bn": (None, [P, P, P, P, P, S, S, P, P]),
+            "or_dwconv_bn_silu": (None, [P, S, S, S, P, P, P]),
+            "or_rel_pos_table": (None, [S, S, P]),
+            "or_linear_f32": (None, [P, S, S, P, P, S, P]),
+            "or_subsampling_frames": (S, [S, S, S]),
+            "or_subsampling": (S, [P, S, S, S, S, S, P, P, P, P, P, P, P, P, S, P]),
+            "or_attn_core_int8": (None, [P, P, S, S, S, P, P, F, P]),
+            "or_conformer_layer": (None, [P, S, P, P, S, S, S, S, S, I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -154,3 +167,134 @@ def gemm_ep_vnni(wq, sq, out, inp, group, x, xs, gsum, y, ep=EP_STORE, alpha=0.0
     n = x.shape[0]
     lib().or_gemm_ep_vnni(_p(wq), _p(sq), out, inp, group, _p(x), _p(xs), _p(gsum), n, _p(y), ep, alpha, threads,
                           blocks_mult)
+
+
+# ------------------------------------------------------------------------------------------------ encoder side
+
+def _f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def row_mean_var(x):
+    x = _f32(x)
+    m, v = C.c_float(), C.c_float()
+    lib().or_row_mean_var(_p(x), x.size, C.byref(m), C.byref(v))
+    return m.value, v.value
+
+
+def layer_norm(x, g, b):
+    x, g, b = _f32(x), _f32(g), _f32(b)
+    n, d = x.shape
+    y = np.empty_like(x)
+    lib().or_layer_norm(_p(x), n, d, _p(g), _p(b), _p(y))
+    return y
+
+
+def quantize_normed(x, g, b, group):
+    x, g, b = _f32(x), _f32(g), _f32(b)
+    n, inp = x.shape
+    ng = inp // group
+    q = np.empty((n, inp), np.int8)
+    s = np.empty((n, ng), np.float32)
+    gs = np.empty((n, ng), np.int32)
+    lib().or_quantize_normed(_p(x), n, inp, group, _p(g), _p(b), _p(q), _p(s), _p(gs))
+    return q, s, gs
+
+
+def exp_row_scaled(row, scale):
+    """Returns (exponentials, sum); the input is not modified."""
+    r = _f32(row).copy()
+    s = lib().or_exp_row_scaled(_p(r), r.size, scale)
+    return r, s
+
+
+def glu(gbuf):
+    gbuf = _f32(gbuf)
+    n, d2 = gbuf.shape
+    out = np.empty((n, d2 // 2), np.float32)
+    lib().or_glu(_p(gbuf), n, d2 // 2, _p(out))
+    return out
+
+
+def fold_bn(dw, gamma, beta, mean, var):
+    dw = _f32(dw)
+    d, k = dw.shape
+    dw_t = np.empty((k, d), np.float32)
+    bias = np.empty(d, np.float32)
+    lib().or_fold_bn(_p(dw), _p(_f32(gamma)), _p(_f32(beta)), _p(_f32(mean)), _p(_f32(var)), d, k, _p(dw_t),
+                     _p(bias))
+    return dw_t, bias
+
+
+def dwconv_bn_silu(a, dw_t, dw_bias):
+    a, dw_t, dw_bias = _f32(a), _f32(dw_t), _f32(dw_bias)
+    t, d = a.shape
+    out = np.empty_like(a)
+    lib().or_dwconv_bn_silu(_p(a), t, d, dw_t.shape[0], _p(dw_t), _p(dw_bias), _p(out))
+    return out
+
+
+def rel_pos_table(t, d):
+    out = np.empty((2 * t - 1, d), np.float32)
+    lib().or_rel_pos_table(t, d, _p(out))
+    return out
+
+
+def linear_f32(x, w, b=None):
+    x, w = _f32(x), _f32(w)
+    n, in_f = x.shape
+    out_f = w.shape[0]
+    y = np.empty((n, out_f), np.float32)
+    lib().or_linear_f32(_p(x), n, in_f, _p(w), _p(None if b is None else _f32(b)), out_f, _p(y))
+    return y
+
+
+def subsampling_frames(t, k=3, s=2):
+    return lib().or_subsampling_frames(t, k, s)
+
+
+def subsampling(feats, sp):
+    """sp: dict with conv0_w [k*k, C], conv0_b [C], dw_w [2, k*k, C], dw_b [2, C], pw_w [2, C, C], pw_b [2, C],
+    lin_w [d, f3*C], lin_b [d], k, s."""
+    feats = _f32(feats)
+    t, n_mels = feats.shape
+    c = sp["conv0_b"].shape[0]
+    d = sp["lin_b"].shape[0]
+    t3 = subsampling_frames(t, sp["k"], sp["s"])
+    out = np.empty((t3, d), np.float32)
+    keep = [_f32(sp[k]) for k in ("conv0_w", "conv0_b", "dw_w", "dw_b", "pw_w", "pw_b", "lin_w", "lin_b")]
+    lib().or_subsampling(_p(feats), t, n_mels, c, sp["k"], sp["s"], *[_p(a) for a in keep], d, _p(out))
+    return out
+
+
+def attn_core_int8(qkv, rel_k, heads, bias_u, bias_v, scaling=None):
+    qkv, rel_k = _f32(qkv), _f32(rel_k)
+    t, d3 = qkv.shape
+    d = d3 // 3
+    if scaling is None:
+        scaling = float(np.float32(1.0) / np.sqrt(np.float32(d // heads)))
+    ctx = np.empty((t, d), np.float32)
+    lib().or_attn_core_int8(_p(qkv), _p(rel_k), t, d, heads, _p(_f32(bias_u)), _p(_f32(bias_v)), scaling, _p(ctx))
+    return ctx
+
+
+LAYER_LINEARS = ("ff1_w1", "ff1_w2", "qkv", "o", "pos", "pw1", "pw2", "ff2_w1", "ff2_w2")
+LAYER_NORMS = ("ff1", "attn", "conv", "ff2", "out")
+
+
+def conformer_layer(x, pos_emb, lp, heads, kconv=9, group=128, threads=None):
+    """One layer in place on a copy of x [t, d]; lp: dict with the 9 ternary linears as (trits int8 [out, inp],
+    scales f32 [out, inp/group]) under LAYER_LINEARS, norms {name: (g, b)}, bias_u, bias_v, dw_t, dw_bias."""
+    x = _f32(x).copy()
+    t, d = x.shape
+    ff = lp["ff1_w1"][0].shape[0]
+    keep = [np.ascontiguousarray(lp[n][0], np.int8) for n in LAYER_LINEARS]
+    keep += [_f32(lp[n][1]) for n in LAYER_LINEARS]
+    for n in LAYER_NORMS:
+        keep += [_f32(lp["norms"][n][0]), _f32(lp["norms"][n][1])]
+    keep += [_f32(lp["bias_u"]), _f32(lp["bias_v"]), _f32(lp["dw_t"]), _f32(lp["dw_bias"])]
+    ptrs = (C.c_void_p * len(keep))(*[a.ctypes.data for a in keep])
+    pos_emb = _f32(pos_emb)
+    lib().or_conformer_layer(_p(x), t, _p(pos_emb), ptrs, d, heads, ff, kconv, group,
+                             threads or os.cpu_count() or 1)
+    return x

@@ -18,6 +18,21 @@
  *   or_exp_poly : relative error < 3e-7 against exp in double (tensor.rs:1018-1030).
  *   or_lcg : the numpy jump-ahead generator (voxrt_amd/synth.py) must reproduce its stream exactly.
  *   or_gemm_vnni_range (CPU baseline) : bit-identical to or_gemm_scalar_range on the x86_kernels.rs grid.
+ *
+ * Encoder side (encoder_oracle.c):
+ *   or_row_mean_var / or_layer_norm : float64 LayerNorm within 1e-5; constant rows give exactly b; a numpy float32
+ *       walk of the same lane order on rows with tails.
+ *   or_quantize_normed : equals or_quantize(or_layer_norm(x)) element for element.
+ *   or_exp_row_scaled : every element within 3e-7 of exp in float64, the arg-max element exactly 1, the sum within
+ *       1e-6 of the float64 sum.
+ *   or_glu / or_dwconv_bn_silu / or_fold_bn : float64 a*sigmoid(b); float64 depthwise conv with the unfolded
+ *       BatchNorm and SiLU (torch conv1d).
+ *   or_rel_pos_table : float64 sin/cos within 1e-6 (ulp-level agreement with the libm crate is parity unpinned).
+ *   or_linear_f32 : float64 matmul within 1e-5 relative; a numpy float32 walk of the lane order.
+ *   or_subsampling : torch float64 conv2d / depthwise conv2d / linear on the [T, F] input (NCHW) within 1e-4.
+ *   or_attn_core_int8 : exact int32 score sums (int64 matmul), float64 relative-position softmax attention within
+ *       the int8 quantization error, the position band checked by a one-hot relative table.
+ *   or_conformer_layer : equals the composition of the pinned pieces above, called one by one.
  */
 #ifndef VOXRT_ORACLE_H
 #define VOXRT_ORACLE_H
@@ -62,6 +77,28 @@ void or_gemm_vnni_range(const int8_t *wq, const float *scales_q, size_t out, siz
 void or_gemm_ep_vnni(const int8_t *wq, const float *scales_q, size_t out, size_t inp, size_t group,
                      const int8_t *x, const float *xs, const int32_t *gsum, size_t n, float *y, int ep, float alpha,
                      int threads, size_t blocks_mult);
+
+/* Encoder side (encoder_oracle.c) */
+void or_row_mean_var(const float *x, size_t d, float *mean, float *var);
+void or_layer_norm(const float *x, size_t n, size_t d, const float *g, const float *b, float *y);
+void or_quantize_normed(const float *x, size_t n, size_t inp, size_t group, const float *g, const float *b,
+                        int8_t *q, float *scales, int32_t *gsum);
+float or_exp_row_scaled(float *row, size_t n, float scale);
+void or_glu(const float *gbuf, size_t n, size_t d, float *out);
+void or_fold_bn(const float *dw, const float *gamma, const float *beta, const float *mean, const float *var,
+                size_t d, size_t k, float *dw_t, float *dw_bias);
+void or_dwconv_bn_silu(const float *a, size_t t, size_t d, size_t k, const float *dw_t, const float *dw_bias,
+                       float *out);
+void or_rel_pos_table(size_t t, size_t d, float *out);
+void or_linear_f32(const float *x, size_t n, size_t in_f, const float *w, const float *b, size_t out_f, float *y);
+size_t or_subsampling_frames(size_t t, size_t k, size_t s);
+size_t or_subsampling(const float *feats, size_t t, size_t n_mels, size_t c, size_t k, size_t s, const float *conv0_w,
+                      const float *conv0_b, const float *dw_w, const float *dw_b, const float *pw_w,
+                      const float *pw_b, const float *lin_w, const float *lin_b, size_t d_model, float *out);
+void or_attn_core_int8(const float *qkv, const float *rel_k, size_t t, size_t d, size_t h, const float *bias_u,
+                       const float *bias_v, float scaling, float *ctx);
+void or_conformer_layer(float *x, size_t t, const float *pos_emb, const void *const *params, size_t d, size_t heads,
+                        size_t ff, size_t kconv, size_t group, int threads);
 
 #ifdef __cplusplus
 }

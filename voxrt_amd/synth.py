@@ -115,3 +115,63 @@ def ref_acts(rng: Lcg, n: int, inp: int, div: float = 100.0, off: float = 10.0) 
     """The reference tests' activations ``(lcg % 2001) as f32 / div - off`` (tests/kernels.rs:42-44)."""
     k = (rng.take(n * inp) % 2001).astype(np.float32)
     return (k / np.float32(div) - np.float32(off)).astype(np.float32).reshape(n, inp)
+
+
+# ------------------------------------------------------------------------------- encoder parameters (synthetic)
+#
+# Random FastConformer weights for the encoder workloads (no checkpoint is available): ternary linears in the
+# thrush-ternary-v2 format (packed trits + f16 scales per (row, 128-column group)), LayerNorm, relative-position
+# biases, depthwise conv with BatchNorm statistics, and the subsampling convolutions. numpy's PCG64 seeded per
+# (layer, tensor), so every run and both sides of a parity test see the same weights.
+
+LAYER_LINEARS = ("ff1_w1", "ff1_w2", "qkv", "o", "pos", "pw1", "pw2", "ff2_w1", "ff2_w2")
+LAYER_NORMS = ("ff1", "attn", "conv", "ff2", "out")
+
+
+def _rng(layer: int, tensor: int) -> np.random.Generator:
+    return np.random.default_rng([0x766F7872, layer, tensor])
+
+
+def synth_ternary_linear(layer: int, tensor: int, out: int, inp: int, group: int = 128):
+    """(packed uint8 [out, ceil(inp/5)], f16 scale codes uint16 [out, inp/group]); trits with P(0)=0.4,
+    P(+-1)=0.3 and scales uniform in [0.01, 0.05]."""
+    r = _rng(layer, tensor)
+    u = r.integers(0, 10, size=(out, inp), dtype=np.int8)
+    trits = np.zeros((out, inp), np.int8)
+    trits[(u >= 4) & (u <= 6)] = -1
+    trits[u >= 7] = 1
+    s = r.uniform(0.01, 0.05, size=(out, inp // group)).astype(np.float16).view(np.uint16)
+    return pack_rows(trits), s
+
+
+def synth_layer(layer: int, d: int = 1024, ff: int = 4096, heads: int = 8, kconv: int = 9, group: int = 128):
+    """One FastConformer layer's parameters as the model file holds them (before BatchNorm folding)."""
+    shapes = {"ff1_w1": (ff, d), "ff1_w2": (d, ff), "qkv": (3 * d, d), "o": (d, d), "pos": (d, d),
+              "pw1": (2 * d, d), "pw2": (d, d), "ff2_w1": (ff, d), "ff2_w2": (d, ff)}
+    p = {"linears": {n: synth_ternary_linear(layer, i, *shapes[n], group) for i, n in enumerate(LAYER_LINEARS)}}
+    r = _rng(layer, 100)
+    f32 = np.float32
+    p["norms"] = {n: ((1.0 + 0.1 * r.standard_normal(d)).astype(f32), (0.1 * r.standard_normal(d)).astype(f32))
+                  for n in LAYER_NORMS}
+    dh = d // heads
+    p["bias_u"] = (0.1 * r.standard_normal((heads, dh))).astype(f32)
+    p["bias_v"] = (0.1 * r.standard_normal((heads, dh))).astype(f32)
+    p["dw"] = (r.standard_normal((d, kconv)) / 3.0).astype(f32)
+    p["bn"] = {"gamma": (1.0 + 0.1 * r.standard_normal(d)).astype(f32), "beta": (0.1 * r.standard_normal(d)).astype(f32),
+               "mean": (0.1 * r.standard_normal(d)).astype(f32), "var": r.uniform(0.5, 1.5, d).astype(f32)}
+    return p
+
+
+def synth_subsampling(d: int = 1024, c: int = 256, k: int = 3, n_mels: int = 128):
+    """Subsampling weights in the layout the reference loads them to (subsampling.rs:32-104): conv0_w [k*k, C],
+    dw_w [2, k*k, C], pw_w [2, C, C] (out, in), lin_w [d, f3*C] with channels-last columns."""
+    r = _rng(1000, 0)
+    f32 = np.float32
+    f3 = n_mels
+    for _ in range(3):
+        f3 = (f3 - 1) // 2 + 1
+    return {"k": k, "s": 2,
+            "conv0_w": (r.standard_normal((k * k, c)) / 3.0).astype(f32), "conv0_b": (0.1 * r.standard_normal(c)).astype(f32),
+            "dw_w": (r.standard_normal((2, k * k, c)) / 3.0).astype(f32), "dw_b": (0.1 * r.standard_normal((2, c))).astype(f32),
+            "pw_w": (r.standard_normal((2, c, c)) / np.sqrt(c)).astype(f32), "pw_b": (0.1 * r.standard_normal((2, c))).astype(f32),
+            "lin_w": (r.standard_normal((d, f3 * c)) / np.sqrt(f3 * c)).astype(f32), "lin_b": (0.1 * r.standard_normal(d)).astype(f32)}
