@@ -11,6 +11,16 @@
  *   vx_quantize                       <- QuantAct::quantize_layout (packed.rs:307-436, quantize_group 527-535)
  *   vx_gemm_ep                        <- kernels::gemm_ep / gemm (kernels/mod.rs:319-362)
  *   vx_gemm_rows_range                <- kernels::gemm_rows_range (kernels/mod.rs:257-282)
+ *   vx_gemm_single                    <- kernels::gemm_single (kernels/mod.rs:285-316)
+ *   vx_quantize_normed                <- TernaryLinear::prepare_normed (ternary_linear.rs:132-155)
+ *   vx_layer_norm                     <- tensor::layer_norm (tensor.rs:700-719)
+ *   vx_glu_dwconv_silu, vx_fold_bn    <- ConvModule::forward_fused / load (encoder.rs:548-573, 590-624)
+ *   vx_linear_f32                     <- tensor::linear (tensor.rs:98-127)
+ *   vx_subsampling*                   <- Subsampling::forward / out_frames (subsampling.rs:114-204)
+ *   vx_rel_pos_table                  <- encoder::rel_pos_table (encoder.rs:760-776)
+ *   vx_attention_core*                <- attn_core_int8 (encoder.rs:317-534)
+ *   vx_encoder_*                      <- GpuEncoder::{load, forward, forward_feats} (metal/mod.rs:446-603) on the
+ *                                        CPU int8 Encoder's operation order (encoder.rs:706-857)
  *   vx_last_error                     <- voxrt_last_error (crates/voxrt-ffi/src/lib.rs:61-74)
  *
  * Conventions (as voxrt-ffi): every call returns a vx_status; on failure a message is kept in a thread-local
@@ -95,6 +105,103 @@ vx_status vx_gemm_ep(const vx_tmat *w, const int8_t *xq, const float *xs_t, cons
 vx_status vx_gemm_rows_range(const vx_tmat *w, const int8_t *xq, const float *xs_t, const int32_t *xgsum_t,
                              int64_t n, float *y, int64_t r0, int64_t r1, int64_t t0, int64_t t1, int ep, float alpha,
                              void *stream);
+
+/* gemm_single: y[n, out] = x . w^T, then y += bias (when not NULL), unfused (kernels/mod.rs:285-316); the decoder's
+ * single-token GEMV. Same operands as vx_gemm_ep. */
+vx_status vx_gemm_single(const vx_tmat *w, const int8_t *xq, const float *xs_t, const int32_t *xgsum_t, int64_t n,
+                         float *y, const float *bias, void *stream);
+
+/* prepare_normed: vx_quantize of LayerNorm(x) (eps 1e-5, biased variance, the reference's summation order;
+ * y = ((x - mean) * inv) * gamma + beta) without writing the normalized rows. gamma, beta float32 [inp]. */
+vx_status vx_quantize_normed(const float *x, int64_t n, int64_t inp, int64_t group, const float *gamma,
+                             const float *beta, int8_t *q, float *scales_t, int32_t *gsum_t, void *stream);
+
+/* layer_norm: y [n, d] = LayerNorm(x [n, d]) with gamma, beta [d]. y may not alias x. */
+vx_status vx_layer_norm(const float *x, int64_t n, int64_t d, const float *gamma, const float *beta, float *y,
+                        void *stream);
+
+/* The conv module between its pointwise convolutions: g [t, 2d] (pointwise_conv1 output) -> out [t, d] =
+ * silu(bias + sum over taps kk of w_t[kk][c] * glu(g)[i + kk - (k-1)/2][c]), glu = a * sigmoid(b) over the two
+ * halves of g, taps outside [0, t) skipped. w_t [k][d] and bias [d] are the BatchNorm-folded taps of vx_fold_bn. */
+vx_status vx_glu_dwconv_silu(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t, const float *bias,
+                             float *out, void *stream);
+
+/* HOST: fold BatchNorm(eval) into the depthwise taps: dw [d][k] (PyTorch [d,1,k]) -> w_t [k][d], bias [d]. */
+vx_status vx_fold_bn(const float *dw, const float *gamma, const float *beta, const float *mean, const float *var,
+                     int64_t d, int64_t k, float *w_t, float *bias);
+
+/* linear: y [n, out_f] = x [n, in_f] . w [out_f, in_f]^T (+ b [out_f] when not NULL), then max(y, 0) when relu. */
+vx_status vx_linear_f32(const float *x, int64_t n, int64_t in_f, const float *w, const float *b, int64_t out_f,
+                        float *y, int relu, void *stream);
+
+/* Subsampling output frames for t input frames (three stride-s convolutions of kernel k, padding (k-1)/2). */
+int64_t vx_subsampling_frames(int64_t t, int64_t k, int64_t s);
+/* Device scratch (float32 elements) that vx_subsampling needs for t frames of nm mel bins and c channels. */
+int64_t vx_subsampling_scratch_floats(int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s);
+/* Subsampling::forward on device buffers: feats [t, nm] -> out [t3, d_model]. Weights as the reference loads them:
+ * conv0_w [k*k, c], conv0_b [c], dw_w [2, k*k, c], dw_b [2, c], pw_w [2, c, c] (out, in), pw_b [2, c],
+ * lin_w [d_model, f3*c] (channels-last columns), lin_b [d_model]. */
+vx_status vx_subsampling(const float *feats, int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s,
+                         const float *conv0_w, const float *conv0_b, const float *dw_w, const float *dw_b,
+                         const float *pw_w, const float *pw_b, const float *lin_w, const float *lin_b, int64_t d_model,
+                         float *scratch, float *out, int64_t *t_out, void *stream);
+
+/* HOST: the relative position table [2t-1, d] (positions t-1 .. -(t-1), sin/cos interleaved per frequency). */
+vx_status vx_rel_pos_table(int64_t t, int64_t d, float *out);
+
+/* Device workspace bytes of vx_attention_core for t frames, model width d and h heads. */
+int64_t vx_attention_ws_bytes(int64_t t, int64_t d, int64_t h);
+/* The int8 attention core of one layer for all heads (head dim 128, 1 <= t <= 1024): qkv [t, 3d] (q | k | v),
+ * rel_k [2t-1, d] (relative_k_proj of the position table), bias_u / bias_v [h, 128], scaling = 1/sqrt(128);
+ * ctx [t, d]. ws: vx_attention_ws_bytes device bytes. */
+vx_status vx_attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h,
+                            const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
+                            void *stream);
+
+/* ---------------------------------------------------------------------------------------------- encoder */
+
+/* Shape of a FastConformer encoder (reference/config.json encoder_config): d = heads * 128. */
+typedef struct vx_encoder_config {
+    int64_t d, heads, ff, kconv, group, n_layers;
+    int64_t n_mels, sub_channels, sub_kernel, sub_stride; /* subsampling (0 if unused) */
+} vx_encoder_config;
+
+/* One layer's weights, HOST pointers, as the model file holds them. Linears in this order: feed_forward1.linear1,
+ * feed_forward1.linear2, q|k|v (q_proj, k_proj, v_proj rows stacked), o_proj, relative_k_proj, pointwise_conv1,
+ * pointwise_conv2, feed_forward2.linear1, feed_forward2.linear2: thrush-ternary-v2 qweight uint8 [out, ceil(inp/5)]
+ * and f16 scales [out, inp/group]. LayerNorms in this order: norm_feed_forward1, norm_self_att, norm_conv,
+ * norm_feed_forward2, norm_out ([d] each). bias_u, bias_v [heads, 128]. dw = depthwise_conv.weight [d, k] and the
+ * BatchNorm (eval) statistics [d], folded at load. */
+typedef struct vx_layer_params {
+    const uint8_t *qweight[9];
+    const uint16_t *scales_f16[9];
+    const float *ln_gamma[5], *ln_beta[5];
+    const float *bias_u, *bias_v;
+    const float *dw, *bn_gamma, *bn_beta, *bn_mean, *bn_var;
+} vx_layer_params;
+
+/* Subsampling weights, HOST pointers, in the layout of vx_subsampling. */
+typedef struct vx_subsampling_params {
+    const float *conv0_w, *conv0_b, *dw_w, *dw_b, *pw_w, *pw_b, *lin_w, *lin_b;
+} vx_subsampling_params;
+
+typedef struct vx_encoder vx_encoder;
+
+vx_status vx_encoder_create(const vx_encoder_config *cfg, vx_encoder **enc);
+/* Upload layer `layer`'s weights (every layer must be set before a forward). */
+vx_status vx_encoder_set_layer(vx_encoder *enc, int64_t layer, const vx_layer_params *p);
+vx_status vx_encoder_set_subsampling(vx_encoder *enc, const vx_subsampling_params *p);
+/* 1 (default): each frame count's layer stack is captured once into a hipGraph and replayed on a non-NULL stream;
+ * 0: kernels are launched one by one. */
+vx_status vx_encoder_use_graphs(vx_encoder *enc, int on);
+/* The layer stack (GpuEncoder::forward): x [t, d] (device, the subsampling output) -> out [t, d] (may alias x);
+ * 1 <= t <= 1024. A workspace is kept per distinct t. Calls on one encoder must not overlap. */
+vx_status vx_encoder_forward(vx_encoder *enc, const float *x, float *out, int64_t t, void *stream);
+/* Subsampling + layers (GpuEncoder::forward_feats): feats [t_in, n_mels] (device) -> out [t_out, d] (device, sized
+ * for vx_subsampling_frames(t_in, sub_kernel, sub_stride) rows). */
+vx_status vx_encoder_forward_feats(vx_encoder *enc, const float *feats, int64_t t_in, float *out, int64_t *t_out,
+                                   void *stream);
+void vx_encoder_free(vx_encoder *enc);
 
 #ifdef __cplusplus
 }

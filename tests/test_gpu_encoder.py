@@ -1,0 +1,223 @@
+"""The encoder-side HIP kernels and the whole encoder == the oracle, bit for bit, through the C ABI.
+
+Restates, for the HIP path, the reference's per-piece exactness (the int8 encoder's fused LayerNorm quantizer,
+ternary_linear.rs:132-155; glue of encoder.rs and tensor.rs; the int8 attention core, encoder.rs:317-534; the f32
+subsampling, subsampling.rs:124-204) and its GPU-encoder test (metal_encoder.rs: GPU encoder vs CPU encoder on the
+same input; here bit-exact against the CPU int8 restatement instead of a tolerance), plus the single-token GEMV of
+kernels.rs:271-316 (gemv_equals_scalar_exactly).
+"""
+import numpy as np
+import pytest
+
+from voxrt_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    import voxrt_amd as vx
+
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    assert vx.detect() == vx.Kernel.Hip, "no gfx950 device"
+    vx.kernels.check(vx.lib().vx_init(0))
+    return torch.device("cuda:0")
+
+
+def _t(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _bits_equal(got, want, what):
+    g = np.ascontiguousarray(got, np.float32).view(np.uint32).ravel()
+    w = np.ascontiguousarray(want, np.float32).view(np.uint32).ravel()
+    bad = np.flatnonzero(g != w)
+    assert bad.size == 0, (f"{what}: {bad.size} of {g.size} differ, first at {bad[0]}: got "
+                           f"{np.asarray(got).ravel()[bad[0]]!r} want {np.asarray(want).ravel()[bad[0]]!r}")
+
+
+def _x(seed, *shape, scale=1.0):
+    return (scale * np.random.default_rng(seed).standard_normal(shape)).astype(np.float32)
+
+
+@pytest.mark.parametrize("n,inp,group", [(1, 1024, 128), (37, 1024, 128), (338, 1024, 128), (5, 1024, 1024),
+                                         (9, 2048, 64), (3, 192, 64)])
+def test_quantize_normed_equals_oracle(dev, orc, n, inp, group):
+    import voxrt_amd as vx
+
+    x = _x(n + inp, n, inp, scale=2.0) + np.float32(0.3)
+    g = _x(1, inp) * np.float32(0.2) + np.float32(1.0)
+    b = _x(2, inp) * np.float32(0.2)
+    want_q, want_s, want_g = orc.quantize_normed(x, g, b, group)
+    a = vx.QuantAct.quantize_normed(_t(x, dev), _t(g, dev), _t(b, dev), group)
+    np.testing.assert_array_equal(a.x.cpu().numpy(), want_q)
+    _bits_equal(a.scales.cpu().numpy(), want_s, "scales")
+    np.testing.assert_array_equal(a.gsum.cpu().numpy(), want_g)
+
+
+@pytest.mark.parametrize("n,d", [(1, 1024), (65, 1024), (7, 1027), (3, 20)])
+def test_layer_norm_equals_oracle(dev, orc, n, d):
+    from voxrt_amd import encoder as E
+
+    x = _x(d, n, d, scale=3.0)
+    g = _x(3, d) * np.float32(0.1) + np.float32(1.0)
+    b = _x(4, d) * np.float32(0.1)
+    got = E.layer_norm(_t(x, dev), _t(g, dev), _t(b, dev)).cpu().numpy()
+    _bits_equal(got, orc.layer_norm(x, g, b), f"layer_norm n={n} d={d}")
+
+
+def test_fold_bn_equals_oracle(orc):
+    from voxrt_amd import encoder as E
+
+    d, k = 1024, 9
+    dw = _x(5, d, k, scale=0.3)
+    gamma, beta, mean = _x(6, d) * 0.1 + 1, _x(7, d) * 0.1, _x(8, d) * 0.1
+    var = np.random.default_rng(9).uniform(0.5, 1.5, d).astype(np.float32)
+    w1, b1 = E.fold_bn(dw, gamma, beta, mean, var)
+    w2, b2 = orc.fold_bn(dw, gamma, beta, mean, var)
+    _bits_equal(w1, w2, "taps")
+    _bits_equal(b1, b2, "bias")
+
+
+@pytest.mark.parametrize("t,d", [(1, 64), (4, 64), (338, 1024), (750, 1024)])
+def test_glu_dwconv_silu_equals_oracle(dev, orc, t, d):
+    from voxrt_amd import encoder as E
+
+    g = _x(t + d, t, 2 * d, scale=2.0)
+    dw = _x(10, d, 9, scale=0.3)
+    gamma, beta, mean = _x(11, d) * 0.1 + 1, _x(12, d) * 0.1, _x(13, d) * 0.1
+    var = np.random.default_rng(14).uniform(0.5, 1.5, d).astype(np.float32)
+    w_t, bias = orc.fold_bn(dw, gamma, beta, mean, var)
+    want = orc.dwconv_bn_silu(orc.glu(g), w_t, bias)
+    got = E.glu_dwconv_silu(_t(g, dev), _t(w_t, dev), _t(bias, dev)).cpu().numpy()
+    _bits_equal(got, want, f"glu/dwconv t={t} d={d}")
+
+
+@pytest.mark.parametrize("n,in_f,out_f,relu", [(1, 37, 9, False), (1, 4096, 1024, False), (6, 256, 40, True),
+                                               (13, 4099, 5, False), (700, 256, 256, True), (94, 4096, 1024, False)])
+def test_linear_f32_equals_oracle(dev, orc, n, in_f, out_f, relu):
+    from voxrt_amd import encoder as E
+
+    x, w, b = _x(15, n, in_f), _x(16, out_f, in_f, scale=0.05), _x(17, out_f)
+    want = orc.linear_f32(x, w, b)
+    if relu:
+        want = np.where(want > 0, want, np.float32(0)).astype(np.float32)
+    got = E.linear_f32(_t(x, dev), _t(w, dev), _t(b, dev), relu=relu).cpu().numpy()
+    _bits_equal(got, want, f"linear {n}x{in_f}x{out_f}")
+
+
+@pytest.mark.parametrize("t,n_mels,c,d", [(41, 40, 16, 96), (2704, 128, 256, 1024)])
+def test_subsampling_equals_oracle(dev, orc, t, n_mels, c, d):
+    from voxrt_amd import encoder as E
+
+    sp = synth.synth_subsampling(d=d, c=c, n_mels=n_mels)
+    feats = _x(18, t, n_mels)
+    want = orc.subsampling(feats, sp)
+    sub = E.Subsampling(sp, n_mels, dev)
+    got = sub.forward(_t(feats, dev)).cpu().numpy()
+    assert got.shape == want.shape == (sub.out_frames(t), d)
+    _bits_equal(got, want, f"subsampling t={t}")
+
+
+def test_rel_pos_table_equals_oracle(orc):
+    from voxrt_amd import encoder as E
+
+    for t in (1, 9, 338):
+        _bits_equal(E.rel_pos_table(t, 1024), orc.rel_pos_table(t, 1024), f"pos table t={t}")
+
+
+@pytest.mark.parametrize("t,heads", [(1, 1), (5, 2), (29, 2), (338, 8), (750, 8)])
+def test_attention_core_equals_oracle(dev, orc, t, heads):
+    from voxrt_amd import encoder as E
+
+    d = heads * 128
+    qkv = _x(19 + t, t, 3 * d)
+    rel = _x(20 + t, 2 * t - 1, d)
+    bu, bv = _x(21, heads, 128, scale=0.3), _x(22, heads, 128, scale=0.3)
+    want = orc.attn_core_int8(qkv, rel, heads, bu, bv)
+    got = E.attention_core(_t(qkv, dev), _t(rel, dev), heads, _t(bu, dev), _t(bv, dev)).cpu().numpy()
+    _bits_equal(got, want, f"attention t={t} heads={heads}")
+
+
+def test_gemm_single_equals_scalar(dev, orc):
+    """kernels.rs:271-316: int8 rows (lcg % 255 as i8), scales (lcg % 100)/1000 + 0.001, x = (lcg % 2001)/100 - 10,
+    bias (lcg % 100)/10, one token; y == scalar kernel + bias, bit for bit."""
+    import torch
+
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(99)
+    for out, inp in [(8194, 640), (2560, 640), (13, 128), (8, 256), (3, 128)]:
+        rows = (rng.take(out * inp) % 255).astype(np.uint8).view(np.int8).reshape(out, inp)
+        scales = ((rng.take(out * inp // 128) % 100).astype(np.float32) / np.float32(1000.0)
+                  + np.float32(0.001)).astype(np.float32).reshape(out, inp // 128)
+        x = ((rng.take(inp) % 2001).astype(np.float32) / np.float32(100.0) - np.float32(10.0)).reshape(1, inp)
+        bias = ((rng.take(out) % 100).astype(np.float32) / np.float32(10.0)).astype(np.float32)
+        q, xs, _ = orc.quantize(x, 128)
+        want = (orc.gemm(rows, scales, q, xs, 128) + bias[None, :]).astype(np.float32)
+        w = vx.TernaryMatrix.from_i8_rows(rows, scales, out, inp, 128)
+        xa = vx.QuantAct.quantize(_t(x, dev), 128)
+        y = torch.zeros((1, out), dtype=torch.float32, device=dev)
+        vx.kernels.gemm_single(w, xa, y, _t(bias, dev))
+        _bits_equal(y.cpu().numpy(), want, f"gemv out={out} inp={inp}")
+
+
+def _oracle_layer(orc, p):
+    d = p["norms"]["out"][0].size
+    lp = {}
+    for n, (q, s) in p["linears"].items():
+        inp = s.shape[1] * 128
+        lp[n] = (orc.unpack_rows(q, inp), orc.f16_to_f32(s))
+    lp["norms"] = p["norms"]
+    lp["bias_u"], lp["bias_v"] = p["bias_u"], p["bias_v"]
+    lp["dw_t"], lp["dw_bias"] = orc.fold_bn(p["dw"], **p["bn"])
+    assert lp["dw_t"].shape[1] == d
+    return lp
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_encoder_layers_equal_oracle(dev, orc, graphs):
+    """Two full-width layers (d=1024, 8 heads, FFN 4096, conv kernel 9) at t=64: the device layer stack equals the
+    CPU int8 layer restatement bit for bit; with graphs, three replays in a row agree with it too."""
+    from voxrt_amd import encoder as E
+
+    t, L = 64, 2
+    params = [synth.synth_layer(i) for i in range(L)]
+    enc = E.Encoder(n_layers=L)
+    enc.use_graphs(graphs)
+    for i, p in enumerate(params):
+        enc.set_layer(i, p)
+    x = _x(23, t, 1024)
+    want = x.copy()
+    pos = orc.rel_pos_table(t, 1024)
+    for p in params:
+        want = orc.conformer_layer(want, pos, _oracle_layer(orc, p), heads=8)
+    xd = _t(x, dev)
+    for rep in range(3 if graphs else 1):
+        got = enc.forward(xd).cpu().numpy()
+        _bits_equal(got, want, f"encoder layers (graphs={graphs}, pass {rep})")
+    enc.free()
+
+
+def test_encoder_feats_equal_oracle(dev, orc):
+    """Subsampling + one layer from log-mel features (t_in = 200 -> 25 frames), bit-exact."""
+    from voxrt_amd import encoder as E
+
+    t_in = 200
+    p = synth.synth_layer(5)
+    sp = synth.synth_subsampling()
+    enc = E.Encoder(n_layers=1)
+    enc.set_layer(0, p)
+    enc.set_subsampling(sp)
+    feats = _x(24, t_in, 128)
+    x = orc.subsampling(feats, sp)
+    t = x.shape[0]
+    want = orc.conformer_layer(x, orc.rel_pos_table(t, 1024), _oracle_layer(orc, p), heads=8)
+    got = enc.forward_feats(_t(feats, dev)).cpu().numpy()
+    assert got.shape == (t, 1024) == (enc.out_frames(t_in), 1024)
+    _bits_equal(got, want, "encoder from features")
+    enc.free()

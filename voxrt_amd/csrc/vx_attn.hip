@@ -1,0 +1,335 @@
+// vx_attn.hip — the int8 relative-position attention core of one layer (attn_core_int8, encoder.rs:317-534), all
+// heads in two launches, equal to the CPU path bit for bit.
+//
+// Reference semantics, per head h (dh = 128 columns of q | k | v):
+//   qu = q + bias_u, qv = q + bias_v, quantized per token in one group of dh (QuantAct::from_rows);
+//   keys, relative positions (rows of the relative_k_proj output) and vT (one row per channel over the tokens,
+//   zero-padded to t16) quantized per row in one group (TernaryMatrix::from_f32_rows, packed.rs:203-249);
+//   S1[i][j] = fma((float)(qu_i . k_j), s_qu[i] * s_k[j], 0), S2[i][p] = fma((float)(qv_i . r_p), s_qv[i] * s_r[p], 0)
+//   (single-group folds of kernels/mod.rs:166-210); score = S1[i][j] + S2[i][t-1-i+j];
+//   e = exp_row_scaled(score, 1/sqrt(dh)) (tensor.rs:810-826: max of score*scale, exp_poly(score*scale - max), four
+//   lane sums over quads, hsum4, the tail in order); the row e (zero-padded to t16) quantized in one group, its scale
+//   multiplied by 1/sum; ctx[i][h*dh + c] = fma((float)(p_i . v_c), s_p[i] * s_v[c], 0).
+//
+// Kernels:
+//   attn_rows_kernel  : one wavefront per 128-wide row: q+bias_u, q+bias_v, k (tokens), relative rows; quantize.
+//   attn_vt_kernel    : one wavefront per (head, channel): the column of v over the tokens, quantized.
+//   attn_core_kernel  : one workgroup per (head, 16 query rows). Content scores for all keys and the position band
+//                       [t-1-i_max, 2t-2-i0] through v_mfma_i32_16x16x64_i8 into LDS; softmax in LDS (the four
+//                       running sums per row on four lanes, so the order is the reference's); the probabilities
+//                       quantized into LDS; P . vT through the same MFMA; ctx written in place in [t][d].
+#include "vx_internal.h"
+
+namespace vx {
+
+constexpr int kDh = 128;
+
+struct AttnWs {  // device workspace, see attn_ws_bytes
+    int8_t *qu, *qv, *kq, *rq, *vq;
+    float *qus, *qvs, *ks, *rs, *vs;
+};
+
+// round up helpers
+__host__ __device__ inline int up16(int x) { return (x + 15) / 16 * 16; }
+__host__ __device__ inline int up64(int x) { return (x + 63) / 64 * 64; }
+
+struct AttnDims {
+    int t, d, h, np, tp, rp, tv;
+    __host__ __device__ AttnDims(int t_, int d_, int h_) : t(t_), d(d_), h(h_) {
+        np = 2 * t - 1;
+        tp = up16(t);       // token rows (queries, keys)
+        rp = up16(np) + 16; // relative rows, one spare block for the band alignment
+        tv = up64(t);       // K extent of the context product
+    }
+};
+
+__device__ inline int8_t q_code(float x, float inv) {
+    float v = __builtin_rintf(x * inv);
+    if (!(v == v)) return 0;
+    v = v < -127.0f ? -127.0f : v;
+    v = v > 127.0f ? 127.0f : v;
+    return (int8_t)(int)v;
+}
+
+__device__ inline float wave_max(float m) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    return m;
+}
+
+// Quantize the 128 values a (two per lane: columns 2*lane, 2*lane+1) into dst[128]; returns the scale.
+__device__ inline float quant128(float a0, float a1, int lane, int8_t *dst) {
+    const float m = wave_max(fmaxf(fabsf(a0), fabsf(a1)));
+    const float s = m == 0.0f ? 1.0f : m / 127.0f;
+    const float inv = 1.0f / s;
+    const int8_t c0 = q_code(a0, inv), c1 = q_code(a1, inv);
+    *(int16_t *)(dst + 2 * lane) = (int16_t)((uint16_t)(uint8_t)c0 | ((uint16_t)(uint8_t)c1 << 8));
+    return s;
+}
+
+// Work items: [0, h*tp) query/key rows (head-major), then [h*tp, h*(tp+rp)) relative rows.
+__global__ __launch_bounds__(256) void attn_rows_kernel(const float *__restrict__ qkv, const float *__restrict__ rel_k,
+                                                       const float *__restrict__ bias_u,
+                                                       const float *__restrict__ bias_v, AttnDims D, AttnWs W) {
+    const int lane = threadIdx.x & 63;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int d3 = 3 * D.d;
+    if (item < D.h * D.tp) {
+        const int h = item / D.tp, i = item % D.tp;
+        const int64_t o = ((int64_t)h * D.tp + i) * kDh;
+        float q0 = 0.0f, q1 = 0.0f, k0 = 0.0f, k1 = 0.0f;
+        if (i < D.t) {
+            const float2 qq = *(const float2 *)(qkv + (int64_t)i * d3 + h * kDh + 2 * lane);
+            const float2 kk = *(const float2 *)(qkv + (int64_t)i * d3 + D.d + h * kDh + 2 * lane);
+            q0 = qq.x;
+            q1 = qq.y;
+            k0 = kk.x;
+            k1 = kk.y;
+        }
+        const float2 bu = *(const float2 *)(bias_u + h * kDh + 2 * lane);
+        const float2 bv = *(const float2 *)(bias_v + h * kDh + 2 * lane);
+        const bool live = i < D.t;
+        const float su = quant128(live ? q0 + bu.x : 0.0f, live ? q1 + bu.y : 0.0f, lane, W.qu + o);
+        const float sv = quant128(live ? q0 + bv.x : 0.0f, live ? q1 + bv.y : 0.0f, lane, W.qv + o);
+        const float sk = quant128(k0, k1, lane, W.kq + o);
+        if (lane == 0) {
+            W.qus[h * D.tp + i] = su;
+            W.qvs[h * D.tp + i] = sv;
+            W.ks[h * D.tp + i] = sk;
+        }
+        return;
+    }
+    const int r = item - D.h * D.tp;
+    if (r >= D.h * D.rp) return;
+    const int h = r / D.rp, p = r % D.rp;
+    float a0 = 0.0f, a1 = 0.0f;
+    if (p < D.np) {
+        const float2 v = *(const float2 *)(rel_k + (int64_t)p * D.d + h * kDh + 2 * lane);
+        a0 = v.x;
+        a1 = v.y;
+    }
+    const float s = quant128(a0, a1, lane, W.rq + ((int64_t)h * D.rp + p) * kDh);
+    if (lane == 0) W.rs[h * D.rp + p] = s;
+}
+
+// One wavefront per (head, channel): vT row = v[i][h*dh + c] for i < t, zero to tv; one group.
+__global__ __launch_bounds__(256) void attn_vt_kernel(const float *__restrict__ qkv, AttnDims D, AttnWs W) {
+    const int lane = threadIdx.x & 63;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= D.h * kDh) return;
+    const int h = item / kDh, c = item % kDh;
+    const float *col = qkv + 2 * D.d + h * kDh + c;
+    const int64_t ld = 3 * (int64_t)D.d;
+    float m = 0.0f;
+    for (int i = lane; i < D.t; i += 64) m = fmaxf(m, fabsf(col[i * ld]));
+    m = wave_max(m);
+    const float s = m == 0.0f ? 1.0f : m / 127.0f;
+    const float inv = 1.0f / s;
+    int8_t *dst = W.vq + ((int64_t)h * kDh + c) * D.tv;
+    for (int i = lane; i < D.tv; i += 64) dst[i] = i < D.t ? q_code(col[i * ld], inv) : (int8_t)0;
+    if (lane == 0) W.vs[h * kDh + c] = s;
+}
+
+// LDS plan of attn_core_kernel (bytes): s1 [16][s1w] f32, s2 [16][s2w] f32, pq [16][tv] int8, row stats.
+__host__ __device__ inline int s1w_of(int t) { return up16(t) + 4; }
+// the band of a block spans at most t + 45 positions after its start is rounded down to a 16-block
+__host__ __device__ inline int s2w_of(int t) { return up16(t + 48) + 4; }
+__host__ __device__ inline size_t core_lds_bytes(int t) {
+    return (size_t)16 * s1w_of(t) * 4 + (size_t)16 * s2w_of(t) * 4 + (size_t)16 * up64(t) + 64 * 4;
+}
+
+__global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, float scaling, float *__restrict__ ctx) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int s1w = s1w_of(D.t), s2w = s2w_of(D.t);
+    float *s1 = (float *)smem;
+    float *s2 = s1 + 16 * s1w;
+    int8_t *pq = (int8_t *)(s2 + 16 * s2w);
+    float *rowv = (float *)(pq + 16 * D.tv);  // [0,16) max, [16,32) 1/sum, [32,48) prob scale
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.y, i0 = blockIdx.x * 16;
+    const int t = D.t;
+    const int imax = min(i0 + 15, t - 1);
+    const int pb0 = (t - 1 - imax) & ~15;        // first position block of the band
+    const int pend = 2 * t - 2 - i0;             // last position used by the block
+    const int npb = (pend - pb0) / 16 + 1;       // position blocks
+    const int nkb = up16(t) / 16;                // key blocks
+
+    // query fragments (A operand, 16x16x64 layout: lane l = row l%16, 16 bytes at 16*(l/16) of each 64-step)
+    const int arow = lane & 15, aq = lane >> 4;
+    const int8_t *qu = W.qu + ((int64_t)h * D.tp + i0 + arow) * kDh + 16 * aq;
+    const int8_t *qv = W.qv + ((int64_t)h * D.tp + i0 + arow) * kDh + 16 * aq;
+    const v4i au0 = *(const v4i *)qu, au1 = *(const v4i *)(qu + 64);
+    const v4i av0 = *(const v4i *)qv, av1 = *(const v4i *)(qv + 64);
+    // D element e of lane l: row 4*(l/16) + e, column l%16
+    const int drow = 4 * aq, dcol = arow;
+    float qus[4], qvs[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        qus[e] = W.qus[h * D.tp + i0 + drow + e];
+        qvs[e] = W.qvs[h * D.tp + i0 + drow + e];
+    }
+    // content scores: key block kb -> s1[row][16*kb + col]
+    for (int kb = wave; kb < nkb; kb += 4) {
+        const int8_t *kr = W.kq + ((int64_t)h * D.tp + kb * 16 + arow) * kDh + 16 * aq;
+        const v4i b0 = *(const v4i *)kr, b1 = *(const v4i *)(kr + 64);
+        v4i acc = {0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au0, b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au1, b1, acc, 0, 0, 0);
+        const float ksv = W.ks[h * D.tp + kb * 16 + dcol];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            s1[(drow + e) * s1w + kb * 16 + dcol] = __builtin_fmaf((float)acc[e], qus[e] * ksv, 0.0f);
+    }
+    // position band: block pb -> s2[row][16*pb' + col], position pb0 + 16*pb' + col
+    for (int pb = wave; pb < npb; pb += 4) {
+        const int p0 = pb0 + pb * 16;
+        const int8_t *rr = W.rq + ((int64_t)h * D.rp + p0 + arow) * kDh + 16 * aq;
+        const v4i b0 = *(const v4i *)rr, b1 = *(const v4i *)(rr + 64);
+        v4i acc = {0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1, acc, 0, 0, 0);
+        const float rsv = W.rs[h * D.rp + p0 + dcol];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            s2[(drow + e) * s2w + pb * 16 + dcol] = __builtin_fmaf((float)acc[e], qvs[e] * rsv, 0.0f);
+    }
+    __syncthreads();
+    const int nrows = imax - i0 + 1;  // valid query rows of the block
+    // score = S1 + S2[t-1-i+j], in place in s1
+    for (int e = tid; e < 16 * t; e += 256) {
+        const int r = e / t, j = e % t;
+        if (r < nrows) {
+            const int i = i0 + r;
+            s1[r * s1w + j] = s1[r * s1w + j] + s2[r * s2w + (t - 1 - i + j - pb0)];
+        }
+    }
+    __syncthreads();
+    // row max of score * scaling: 16 lanes per row, wave w rows 4w .. 4w+3
+    {
+        const int r = wave * 4 + (lane >> 4), l16 = lane & 15;
+        float m = -INFINITY;
+        if (r < nrows)
+            for (int j = l16; j < t; j += 16) m = fmaxf(m, s1[r * s1w + j] * scaling);
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (l16 == 0) rowv[r] = m;
+    }
+    __syncthreads();
+    for (int e = tid; e < 16 * t; e += 256) {
+        const int r = e / t, j = e % t;
+        if (r < nrows) s1[r * s1w + j] = exp_poly(s1[r * s1w + j] * scaling - rowv[r]);
+    }
+    __syncthreads();
+    // row sums in the reference's order: lane 4r + l keeps the running sum of columns j = 4q + l
+    if (wave == 0) {
+        const int r = lane >> 2, l = lane & 3;
+        const int t4 = t / 4 * 4;
+        float acc = 0.0f;
+        if (r < nrows)
+            for (int j = l; j < t4; j += 4) acc += s1[r * s1w + j];
+        const int base = lane & ~3;
+        const float l0 = __shfl(acc, base, 64), l1 = __shfl(acc, base + 1, 64), l2 = __shfl(acc, base + 2, 64),
+                    l3 = __shfl(acc, base + 3, 64);
+        float sum = (l0 + l1) + (l2 + l3);
+        if (r < nrows)
+            for (int j = t4; j < t; j++) sum += s1[r * s1w + j];
+        if (l == 0) rowv[16 + r] = 1.0f / sum;
+    }
+    // probability quantization: amax per row (16 lanes per row), codes into pq, zero to tv
+    {
+        const int r = wave * 4 + (lane >> 4), l16 = lane & 15;
+        float m = 0.0f;
+        if (r < nrows)
+            for (int j = l16; j < t; j += 16) m = fmaxf(m, fabsf(s1[r * s1w + j]));
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float s = m == 0.0f ? 1.0f : m / 127.0f;
+        const float inv = 1.0f / s;
+        for (int j = l16; j < D.tv; j += 16)
+            pq[r * D.tv + j] = (r < nrows && j < t) ? q_code(s1[r * s1w + j], inv) : (int8_t)0;
+        __syncthreads();  // the 1/sum of wave 0 is visible after this barrier
+        if (l16 == 0) rowv[32 + r] = s * rowv[16 + r];
+    }
+    __syncthreads();
+    // context: channel blocks 2*wave, 2*wave+1; K over tv in 64-steps; A = pq rows from LDS, B = vT rows
+    for (int cb = 2 * wave; cb < 2 * wave + 2; cb++) {
+        v4i acc = {0, 0, 0, 0};
+        const int8_t *vr = W.vq + ((int64_t)h * kDh + cb * 16 + arow) * D.tv + 16 * aq;
+        const int8_t *pr = pq + arow * D.tv + 16 * aq;
+        for (int k0 = 0; k0 < D.tv; k0 += 64) {
+            const v4i a = *(const v4i *)(pr + k0);
+            const v4i b = *(const v4i *)(vr + k0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+        }
+        const int c = cb * 16 + dcol;
+        const float vsv = W.vs[h * kDh + c];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int r = drow + e;
+            if (r < nrows)
+                ctx[(int64_t)(i0 + r) * D.d + h * kDh + c] = __builtin_fmaf((float)acc[e], rowv[32 + r] * vsv, 0.0f);
+        }
+    }
+}
+
+size_t attn_ws_bytes(int64_t t, int64_t d, int64_t h) {
+    const AttnDims D((int)t, (int)d, (int)h);
+    const size_t rows = (size_t)h * D.tp, rrows = (size_t)h * D.rp;
+    size_t b = 0;
+    auto add = [&](size_t n) { b += (n + 255) / 256 * 256; };
+    add(rows * kDh);       // qu
+    add(rows * kDh);       // qv
+    add(rows * kDh);       // kq
+    add(rrows * kDh);      // rq
+    add((size_t)h * kDh * D.tv);  // vq
+    add(rows * 4);         // qus
+    add(rows * 4);         // qvs
+    add(rows * 4);         // ks
+    add(rrows * 4);        // rs
+    add((size_t)h * kDh * 4);     // vs
+    return b;
+}
+
+// ctx [t][d] from qkv [t][3d] (q | k | v) and rel_k [2t-1][d]; ws is attn_ws_bytes(t, d, h) device bytes.
+void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h, const float *bias_u,
+                    const float *bias_v, float scaling, void *ws, float *ctx, hipStream_t st) {
+    require(qkv && rel_k && bias_u && bias_v && ws && ctx, "attention: NULL pointer");
+    require(h > 0 && d == h * kDh, "attention: the head dimension must be 128");
+    require(t >= 1 && t <= 1024, "attention: 1 <= t <= 1024 frames");
+    const AttnDims D((int)t, (int)d, (int)h);
+    uint8_t *p = (uint8_t *)ws;
+    auto take = [&](size_t n) {
+        uint8_t *r = p;
+        p += (n + 255) / 256 * 256;
+        return r;
+    };
+    const size_t rows = (size_t)h * D.tp, rrows = (size_t)h * D.rp;
+    AttnWs W;
+    W.qu = (int8_t *)take(rows * kDh);
+    W.qv = (int8_t *)take(rows * kDh);
+    W.kq = (int8_t *)take(rows * kDh);
+    W.rq = (int8_t *)take(rrows * kDh);
+    W.vq = (int8_t *)take((size_t)h * kDh * D.tv);
+    W.qus = (float *)take(rows * 4);
+    W.qvs = (float *)take(rows * 4);
+    W.ks = (float *)take(rows * 4);
+    W.rs = (float *)take(rrows * 4);
+    W.vs = (float *)take((size_t)h * kDh * 4);
+    const int items = (int)(rows + rrows);
+    attn_rows_kernel<<<(unsigned)((items + 3) / 4), 256, 0, st>>>(qkv, rel_k, bias_u, bias_v, D, W);
+    hip_check(hipGetLastError(), "attention rows kernel launch");
+    attn_vt_kernel<<<(unsigned)((h * kDh + 3) / 4), 256, 0, st>>>(qkv, D, W);
+    hip_check(hipGetLastError(), "attention vT kernel launch");
+    const size_t lds = core_lds_bytes((int)t);
+    static bool lds_raised = false;
+    if (!lds_raised) {
+        hip_check(hipFuncSetAttribute((const void *)attn_core_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      160 * 1024),
+                  "attention LDS limit");
+        lds_raised = true;
+    }
+    attn_core_kernel<<<dim3((unsigned)(D.tp / 16), (unsigned)h), 256, lds, st>>>(D, W, scaling, ctx);
+    hip_check(hipGetLastError(), "attention core kernel launch");
+}
+
+}  // namespace vx

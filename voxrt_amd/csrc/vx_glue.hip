@@ -1,0 +1,287 @@
+// vx_glue.hip — the encoder's f32 glue around the int8 GEMMs, in the reference's operation order so that the
+// results equal the CPU path bit for bit:
+//
+//   conv module (encoder.rs:576-628): GLU over channels (a * sigmoid_fast(b), tensor.rs:936-940), the depthwise
+//     time convolution with BatchNorm folded into its taps (encoder.rs:548-573), SiLU — one fused kernel;
+//   the f32 linear of the subsampling (tensor.rs:98-127: four fused lanes per output over 4-column steps, the
+//     tail unfused, (hsum4 + tail) + bias; one token goes through gemv_portable, tensor.rs:284-303);
+//   the subsampling convolutions (subsampling.rs:124-204): 3x3 stride-2 conv 1 -> C with ReLU and the depthwise
+//     3x3 stride-2 convs, channels-last [T, F, C];
+//   host helpers: the BatchNorm fold and the relative position table (encoder.rs:760-776, computed with the C
+//     library's powf/sinf/cosf).
+#include <cmath>
+#include <vector>
+
+#include "vx_internal.h"
+
+namespace vx {
+
+// ---------------------------------------------------------------------------------------- conv module
+
+// out[i][c] = silu(bias[c] + sum over taps kk of w[kk][c] * glu(g[i + kk - pad][c])), taps outside [0, t) skipped,
+// each product and sum rounded separately (encoder.rs:604-624). g is the pointwise_conv1 output [t][2d]; the GLU
+// value of a tap is recomputed per output (it is a pure function of g), so no [t][d] intermediate is stored.
+__global__ __launch_bounds__(256) void glu_dwconv_silu_kernel(const float *__restrict__ g, int t, int d, int k,
+                                                             const float *__restrict__ w_t,
+                                                             const float *__restrict__ bias, float *__restrict__ out) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    const int i = blockIdx.y;
+    if (c >= d) return;
+    const int pad = (k - 1) / 2;
+    float acc = bias[c];
+    for (int kk = 0; kk < k; kk++) {
+        const int j = i + kk - pad;
+        if (j < 0 || j >= t) continue;
+        const float *gj = g + (int64_t)j * 2 * d;
+        const float a = gj[c] * sigmoid_fast(gj[d + c]);
+        acc = acc + w_t[(int64_t)kk * d + c] * a;
+    }
+    out[(int64_t)i * d + c] = silu_fast(acc);
+}
+
+void glu_dwconv_silu(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t, const float *bias, float *out,
+                     hipStream_t st) {
+    require(g && w_t && bias && out, "glu_dwconv: NULL pointer");
+    require(t >= 0 && d > 0 && k > 0 && k % 2 == 1 && t * 2 * d < (1ll << 31), "glu_dwconv: bad shape");
+    if (t == 0) return;
+    glu_dwconv_silu_kernel<<<dim3((unsigned)((d + 255) / 256), (unsigned)t), 256, 0, st>>>(g, (int)t, (int)d, (int)k,
+                                                                                          w_t, bias, out);
+    hip_check(hipGetLastError(), "glu_dwconv kernel launch");
+}
+
+// ---------------------------------------------------------------------------------------- f32 linear
+
+// y[n][out] = x[n][in] . w[out][in]^T + b, each output with the reference tile's lane order: acc[l] =
+// fma(w[c + l], x[c + l], acc[l]) over 4-column steps, tail = sum of unfused w*x in order, y = (hsum4 + tail) + b,
+// optional ReLU. A 256-thread block computes 64 tokens x 64 outputs, a thread 4 x 4 of them, operands staged
+// through LDS in 32-column slabs.
+constexpr int LT = 64, LK = 32;
+
+template <bool RELU>
+__global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict__ x, int n, int in_f,
+                                                        const float *__restrict__ w, const float *__restrict__ b,
+                                                        int out_f, float *__restrict__ y) {
+    __shared__ float xs[LT][LK + 1];
+    __shared__ float ws[LT][LK + 1];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int t0 = blockIdx.y * LT, o0 = blockIdx.x * LT;
+    float acc[4][4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int l = 0; l < 4; l++) acc[a][c][l] = 0.0f;
+    const int c4 = in_f / 4 * 4;
+    for (int k0 = 0; k0 < c4; k0 += LK) {
+        // stage x[t0 .. t0+63][k0 .. k0+31] and w[o0 .. o0+63][k0 .. k0+31] (zero outside; only columns < c4 are
+        // summed into the lanes, the tail is separate)
+        for (int e = threadIdx.x; e < LT * LK; e += 256) {
+            const int r = e / LK, kk = e % LK, col = k0 + kk;
+            const int tt = t0 + r, oo = o0 + r;
+            xs[r][kk] = (tt < n && col < c4) ? x[(int64_t)tt * in_f + col] : 0.0f;
+            ws[r][kk] = (oo < out_f && col < c4) ? w[(int64_t)oo * in_f + col] : 0.0f;
+        }
+        __syncthreads();
+        const int kend = min(LK, c4 - k0);
+        for (int kk = 0; kk < kend; kk += 4) {
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+#pragma unroll
+                    for (int l = 0; l < 4; l++)
+                        acc[a][c][l] = __builtin_fmaf(ws[tx * 4 + c][kk + l], xs[ty * 4 + a][kk + l], acc[a][c][l]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int tt = t0 + ty * 4 + a;
+        if (tt >= n) continue;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int oo = o0 + tx * 4 + c;
+            if (oo >= out_f) continue;
+            float tail = 0.0f;
+            for (int col = c4; col < in_f; col++) tail += w[(int64_t)oo * in_f + col] * x[(int64_t)tt * in_f + col];
+            float v = ((acc[a][c][0] + acc[a][c][1]) + (acc[a][c][2] + acc[a][c][3])) + tail;
+            v = v + (b ? b[oo] : 0.0f);
+            if (RELU) v = v > 0.0f ? v : 0.0f;
+            y[(int64_t)tt * out_f + oo] = v;
+        }
+    }
+}
+
+// One token: gemv_portable (tensor.rs:284-303): rows below out_f/4*4 by dot_lanes8 (fused lanes over 8-column
+// steps, lane-wise a + b, hsum4, tail unfused), the others by dot (8 unfused lane sums summed in order, tail).
+template <bool RELU>
+__global__ void gemv_f32_kernel(const float *__restrict__ x, int in_f, const float *__restrict__ w,
+                                const float *__restrict__ b, int out_f, float *__restrict__ y) {
+    const int o = blockIdx.x * blockDim.x + threadIdx.x;
+    if (o >= out_f) return;
+    const float *wr = w + (int64_t)o * in_f;
+    const int n8 = in_f / 8 * 8, o4 = out_f / 4 * 4;
+    float r;
+    if (o < o4) {
+        float a[4] = {0, 0, 0, 0}, bb[4] = {0, 0, 0, 0};
+        for (int c = 0; c < n8; c += 8)
+            for (int l = 0; l < 4; l++) {
+                a[l] = __builtin_fmaf(x[c + l], wr[c + l], a[l]);
+                bb[l] = __builtin_fmaf(x[c + 4 + l], wr[c + 4 + l], bb[l]);
+            }
+        float p[4];
+        for (int l = 0; l < 4; l++) p[l] = a[l] + bb[l];
+        r = (p[0] + p[1]) + (p[2] + p[3]);
+        for (int c = n8; c < in_f; c++) r += x[c] * wr[c];
+    } else {
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int c = 0; c < n8; c += 8)
+            for (int l = 0; l < 8; l++) acc[l] += x[c + l] * wr[c + l];
+        r = acc[0];
+        for (int l = 1; l < 8; l++) r += acc[l];
+        for (int c = n8; c < in_f; c++) r += x[c] * wr[c];
+    }
+    float v = r + (b ? b[o] : 0.0f);
+    if (RELU) v = v > 0.0f ? v : 0.0f;
+    y[o] = v;
+}
+
+void linear_f32(const float *x, int64_t n, int64_t in_f, const float *w, const float *b, int64_t out_f, float *y,
+                bool relu, hipStream_t st) {
+    require(x && w && y, "linear_f32: NULL pointer");
+    require(n >= 0 && in_f > 0 && out_f > 0 && n * in_f < (1ll << 31) && n * out_f < (1ll << 31) &&
+                out_f * in_f < (1ll << 31),
+            "linear_f32: bad shape");
+    if (n == 0) return;
+    if (n == 1) {
+        auto k = relu ? gemv_f32_kernel<true> : gemv_f32_kernel<false>;
+        k<<<(unsigned)((out_f + 255) / 256), 256, 0, st>>>(x, (int)in_f, w, b, (int)out_f, y);
+    } else {
+        auto k = relu ? linear_f32_kernel<true> : linear_f32_kernel<false>;
+        k<<<dim3((unsigned)((out_f + LT - 1) / LT), (unsigned)((n + LT - 1) / LT)), 256, 0, st>>>(x, (int)n, (int)in_f,
+                                                                                                 w, b, (int)out_f, y);
+    }
+    hip_check(hipGetLastError(), "linear_f32 kernel launch");
+}
+
+// ---------------------------------------------------------------------------------------- subsampling convs
+
+__host__ __device__ inline int conv_out_len(int n, int k, int s, int p) { return (n + 2 * p - k) / s + 1; }
+
+// stage 0 (subsampling.rs:130-160): out[ot][of][ch] = relu(b[ch] + sum over (kt, kf) in order of w[kt*k+kf][ch] *
+// feats[ot*s + kt - p][of*s + kf - p]), out-of-range taps skipped.
+__global__ __launch_bounds__(256) void conv0_kernel(const float *__restrict__ feats, int t, int nm, int k, int s,
+                                                   const float *__restrict__ w, const float *__restrict__ b, int c,
+                                                   int t1, int f1, float *__restrict__ out) {
+    const int pos = blockIdx.x;  // ot * f1 + of
+    const int ot = pos / f1, of = pos % f1, p = (k - 1) / 2;
+    for (int ch = threadIdx.x; ch < c; ch += blockDim.x) {
+        float o = b[ch];
+        for (int kt = 0; kt < k; kt++) {
+            const int it = ot * s + kt - p;
+            if (it < 0 || it >= t) continue;
+            for (int kf = 0; kf < k; kf++) {
+                const int i_f = of * s + kf - p;
+                if (i_f < 0 || i_f >= nm) continue;
+                o = o + w[(kt * k + kf) * c + ch] * feats[(int64_t)it * nm + i_f];
+            }
+        }
+        out[(int64_t)pos * c + ch] = o > 0.0f ? o : 0.0f;
+    }
+}
+
+// depthwise stage (subsampling.rs:163-190): y[ot][of][ch] = b[ch] + sum over (kt, kf) of w[kt*k+kf][ch] *
+// x[ot*s+kt-p][of*s+kf-p][ch], no activation.
+__global__ __launch_bounds__(256) void dwconv2d_kernel(const float *__restrict__ x, int tc, int fc, int k, int s,
+                                                      const float *__restrict__ w, const float *__restrict__ b, int c,
+                                                      int t2, int f2, float *__restrict__ y) {
+    const int pos = blockIdx.x;
+    const int ot = pos / f2, of = pos % f2, p = (k - 1) / 2;
+    for (int ch = threadIdx.x; ch < c; ch += blockDim.x) {
+        float o = b[ch];
+        for (int kt = 0; kt < k; kt++) {
+            const int it = ot * s + kt - p;
+            if (it < 0 || it >= tc) continue;
+            for (int kf = 0; kf < k; kf++) {
+                const int i_f = of * s + kf - p;
+                if (i_f < 0 || i_f >= fc) continue;
+                o = o + w[(kt * k + kf) * c + ch] * x[((int64_t)it * fc + i_f) * c + ch];
+            }
+        }
+        y[(int64_t)pos * c + ch] = o;
+    }
+}
+
+// The whole subsampling (subsampling.rs:124-204) on device buffers; scratch must hold 2 * t1 * f1 * c floats.
+// Returns the output frame count; out is [t3][d_model].
+int64_t subsampling(const float *feats, int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s, const float *conv0_w,
+                    const float *conv0_b, const float *dw_w, const float *dw_b, const float *pw_w, const float *pw_b,
+                    const float *lin_w, const float *lin_b, int64_t d_model, float *scratch, float *out,
+                    hipStream_t st) {
+    require(feats && conv0_w && conv0_b && dw_w && dw_b && pw_w && pw_b && lin_w && lin_b && scratch && out,
+            "subsampling: NULL pointer");
+    require(t > 0 && nm > 0 && c > 0 && k > 0 && s > 0 && c <= 1024, "subsampling: bad shape");
+    const int p = (int)(k - 1) / 2;
+    const int t1 = conv_out_len((int)t, (int)k, (int)s, p), f1 = conv_out_len((int)nm, (int)k, (int)s, p);
+    require((int64_t)t1 * f1 * c < (1ll << 31), "subsampling: input too long");
+    float *a = scratch, *bbuf = scratch + (int64_t)t1 * f1 * c;
+    conv0_kernel<<<(unsigned)(t1 * f1), 256, 0, st>>>(feats, (int)t, (int)nm, (int)k, (int)s, conv0_w,
+                                                                conv0_b, (int)c, t1, f1, a);
+    hip_check(hipGetLastError(), "conv0 kernel launch");
+    int tc = t1, fc = f1;
+    for (int stage = 0; stage < 2; stage++) {
+        const int t2 = conv_out_len(tc, (int)k, (int)s, p), f2 = conv_out_len(fc, (int)k, (int)s, p);
+        dwconv2d_kernel<<<(unsigned)(t2 * f2), 256, 0, st>>>(a, tc, fc, (int)k, (int)s,
+                                                                      dw_w + (int64_t)stage * k * k * c,
+                                                                      dw_b + (int64_t)stage * c, (int)c, t2, f2, bbuf);
+        hip_check(hipGetLastError(), "dwconv2d kernel launch");
+        linear_f32(bbuf, (int64_t)t2 * f2, c, pw_w + (int64_t)stage * c * c, pw_b + (int64_t)stage * c, c, a, true,
+                   st);
+        tc = t2;
+        fc = f2;
+    }
+    linear_f32(a, tc, (int64_t)fc * c, lin_w, lin_b, d_model, out, false, st);
+    return tc;
+}
+
+int64_t subsampling_frames(int64_t t, int64_t k, int64_t s) {
+    const int p = (int)(k - 1) / 2;
+    int n = (int)t;
+    for (int i = 0; i < 3; i++) n = conv_out_len(n, (int)k, (int)s, p);
+    return n;
+}
+
+int64_t subsampling_scratch_floats(int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s) {
+    const int p = (int)(k - 1) / 2;
+    return 2 * (int64_t)conv_out_len((int)t, (int)k, (int)s, p) * conv_out_len((int)nm, (int)k, (int)s, p) * c;
+}
+
+// ---------------------------------------------------------------------------------------- host helpers
+
+// encoder.rs:548-573: s = gamma / sqrt(var + 1e-5); w_t[kk][c] = dw[c][kk] * s; bias = beta - mean * s.
+void fold_bn(const float *dw, const float *gamma, const float *beta, const float *mean, const float *var, int64_t d,
+             int64_t k, float *dw_t, float *dw_bias) {
+    for (int64_t c = 0; c < d; c++) {
+        const float s = gamma[c] / std::sqrt(var[c] + 1e-5f);
+        for (int64_t kk = 0; kk < k; kk++) dw_t[kk * d + c] = dw[c * k + kk] * s;
+        dw_bias[c] = beta[c] - mean[c] * s;
+    }
+}
+
+// encoder.rs:760-776 on the host, float arithmetic with the C library's powf / sinf / cosf.
+void rel_pos_table(int64_t t, int64_t d, float *out) {
+    const int64_t np = 2 * t - 1, half = d / 2;
+    std::vector<float> inv((size_t)half);
+    for (int64_t i = 0; i < half; i++) inv[(size_t)i] = 1.0f / ::powf(10000.0f, 2.0f * (float)i / (float)d);
+    for (int64_t r = 0; r < np; r++) {
+        const float pos = (float)(t - 1 - r);
+        for (int64_t i = 0; i < half; i++) {
+            const float f = inv[(size_t)i] * pos;
+            out[r * d + 2 * i] = ::sinf(f);
+            out[r * d + 2 * i + 1] = ::cosf(f);
+        }
+    }
+}
+
+}  // namespace vx

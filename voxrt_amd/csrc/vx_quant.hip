@@ -5,6 +5,12 @@
 // division), code = clamp(rint(x * inv), -127, 127) with round-half-to-even, NaN -> 0 as Rust's `as i8`;
 // gsum = sum of the codes (exact integer). The codes equal the reference's bit for bit.
 //
+// The LN variants (prepare_normed, ternary_linear.rs:132-155) quantize LayerNorm(x) instead of x: the row's mean and
+// variance are taken in the reference's order (row_mean_var_portable, tensor.rs:331-363: eight running sums over
+// 8-column steps, one per lane of lanes 0-7, combined as hsum4 of the lane pairs, then the tail in order; squares
+// by fma), inv = 1 / sqrt(var + 1e-5), and each element is ((x - mean) * inv) * g + b (tensor.rs:712-719) as it is
+// quantized, so the normalized row never goes to memory.
+//
 // Output layout (QuantAct with its transposed scales, packed.rs:291-294): q int8 [n][inp]; scales_t float32
 // [ng][n_pad] and gsum_t int32 [ng][n_pad] with n_pad = n rounded up to a multiple of 16, pad tokens zero, so a
 // GEMM lane reads the scales of 4 consecutive tokens with one 16-byte load.
@@ -20,17 +26,74 @@ __device__ inline int8_t code_of(float x, float inv) {
     return (int8_t)(int)v;
 }
 
+// Mean and 1/sqrt(var + 1e-5) of one row, in the reference's summation order, broadcast to the wavefront.
+__device__ inline void ln_stats(const float *__restrict__ xr, int d, int lane, float &mean, float &inv) {
+    const int n8 = d / 8 * 8;
+    float s = 0.0f;
+    if (lane < 8)
+        for (int c = lane; c < n8; c += 8) s += xr[c];  // lane l < 4: s0[l]; lane 4 + l: s1[l]
+    float p = s + __shfl(s, lane + 4, 64);              // lanes 0-3: s0[l] + s1[l]
+    float sum = (p + __shfl(p, 1, 64)) + (__shfl(p, 2, 64) + __shfl(p, 3, 64));
+    for (int c = n8; c < d; c++) sum += xr[c];
+    sum = __shfl(sum, 0, 64);
+    mean = sum / (float)d;
+    float q = 0.0f;
+    if (lane < 8)
+        for (int c = lane; c < n8; c += 8) {
+            const float a = xr[c] - mean;
+            q = __builtin_fmaf(a, a, q);
+        }
+    p = q + __shfl(q, lane + 4, 64);
+    float sq = (p + __shfl(p, 1, 64)) + (__shfl(p, 2, 64) + __shfl(p, 3, 64));
+    for (int c = n8; c < d; c++) {
+        const float a = xr[c] - mean;
+        sq += a * a;
+    }
+    sq = __shfl(sq, 0, 64);
+    const float var = sq / (float)d;
+    inv = 1.0f / __builtin_sqrtf(var + 1e-5f);
+}
+
+// y = ((x - mean) * inv) * g + b, one IEEE step at a time
+__device__ inline float ln_apply(float x, float mean, float inv, float g, float b) { return (x - mean) * inv * g + b; }
+
 // Fast path: group = 16 * L with L a power of two up to 64 lanes, or a multiple of 1024. Each lane owns 16
 // consecutive values of a 1024-wide chunk; a group is L adjacent lanes (or whole chunks), reduced with xor
 // shuffles inside the lane group.
-template <int L>
+template <int L, bool LN>
 __global__ __launch_bounds__(256) void quantize_fast_kernel(const float *__restrict__ x, int n, int inp, int group,
                                                           int np, int8_t *__restrict__ q, float *__restrict__ st,
-                                                          int32_t *__restrict__ gt) {
+                                                          int32_t *__restrict__ gt, const float *__restrict__ lg,
+                                                          const float *__restrict__ lb) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= n) return;  // uniform per wavefront
     const float *xr = x + (int64_t)t * inp;
+    float mean = 0.0f, linv = 1.0f;
+    if constexpr (LN) ln_stats(xr, inp, lane, mean, linv);
+    // the 16 values of one lane at column `base`, normalized when LN
+    auto load16 = [&](int base, float (&v)[16]) {
+        const float4 *p = (const float4 *)(xr + base);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 f = p[i];
+            v[4 * i] = f.x;
+            v[4 * i + 1] = f.y;
+            v[4 * i + 2] = f.z;
+            v[4 * i + 3] = f.w;
+        }
+        if constexpr (LN) {
+            const float4 *pg = (const float4 *)(lg + base), *pb = (const float4 *)(lb + base);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 g4 = pg[i], b4 = pb[i];
+                v[4 * i] = ln_apply(v[4 * i], mean, linv, g4.x, b4.x);
+                v[4 * i + 1] = ln_apply(v[4 * i + 1], mean, linv, g4.y, b4.y);
+                v[4 * i + 2] = ln_apply(v[4 * i + 2], mean, linv, g4.z, b4.z);
+                v[4 * i + 3] = ln_apply(v[4 * i + 3], mean, linv, g4.w, b4.w);
+            }
+        }
+    };
     int8_t *qr = q + (int64_t)t * inp;
     const int ng = inp / group;
     const int chunks_per_group = group >= 1024 ? group / 1024 : 1;
@@ -40,12 +103,10 @@ __global__ __launch_bounds__(256) void quantize_fast_kernel(const float *__restr
         for (int cc = 0; cc < chunks_per_group; cc++) {
             const int base = c0 + cc * 1024 + lane * 16;
             if (base < inp) {
-                const float4 *p = (const float4 *)(xr + base);
+                float v[16];
+                load16(base, v);
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float4 v = p[i];
-                    m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-                }
+                for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[i]));
             }
         }
 #pragma unroll
@@ -56,13 +117,13 @@ __global__ __launch_bounds__(256) void quantize_fast_kernel(const float *__restr
         for (int cc = 0; cc < chunks_per_group; cc++) {
             const int base = c0 + cc * 1024 + lane * 16;
             if (base < inp) {
-                const float4 *p = (const float4 *)(xr + base);
+                float v[16];
+                load16(base, v);
                 uint32_t w[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float4 v = p[i];
-                    const int8_t c0_ = code_of(v.x, inv), c1 = code_of(v.y, inv), c2 = code_of(v.z, inv),
-                                 c3 = code_of(v.w, inv);
+                    const int8_t c0_ = code_of(v[4 * i], inv), c1 = code_of(v[4 * i + 1], inv),
+                                 c2 = code_of(v[4 * i + 2], inv), c3 = code_of(v[4 * i + 3], inv);
                     sum += (int)c0_ + (int)c1 + (int)c2 + (int)c3;
                     w[i] = (uint32_t)(uint8_t)c0_ | ((uint32_t)(uint8_t)c1 << 8) | ((uint32_t)(uint8_t)c2 << 16) |
                            ((uint32_t)(uint8_t)c3 << 24);
@@ -87,25 +148,31 @@ __global__ __launch_bounds__(256) void quantize_fast_kernel(const float *__restr
 }
 
 // Any group that divides inp: one group at a time across the wavefront.
+template <bool LN>
 __global__ __launch_bounds__(256) void quantize_generic_kernel(const float *__restrict__ x, int n, int inp,
                                                              int group, int np, int8_t *__restrict__ q,
-                                                             float *__restrict__ st, int32_t *__restrict__ gt) {
+                                                             float *__restrict__ st, int32_t *__restrict__ gt,
+                                                             const float *__restrict__ lg,
+                                                             const float *__restrict__ lb) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= n) return;
     const float *xr = x + (int64_t)t * inp;
     int8_t *qr = q + (int64_t)t * inp;
     const int ng = inp / group;
+    float mean = 0.0f, linv = 1.0f;
+    if constexpr (LN) ln_stats(xr, inp, lane, mean, linv);
+    auto val = [&](int k) { return LN ? ln_apply(xr[k], mean, linv, lg[k], lb[k]) : xr[k]; };
     for (int g = 0; g < ng; g++) {
-        const float *xg = xr + (int64_t)g * group;
+        const int g0 = g * group;
         float m = 0.0f;
-        for (int c = lane; c < group; c += 64) m = fmaxf(m, fabsf(xg[c]));
+        for (int c = lane; c < group; c += 64) m = fmaxf(m, fabsf(val(g0 + c)));
         for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
         const float s = m == 0.0f ? 1.0f : m / 127.0f;
         const float inv = 1.0f / s;
         int sum = 0;
         for (int c = lane; c < group; c += 64) {
-            const int8_t code = code_of(xg[c], inv);
+            const int8_t code = code_of(val(g0 + c), inv);
             qr[(int64_t)g * group + c] = code;
             sum += code;
         }
@@ -128,17 +195,20 @@ __global__ void quantize_pad_kernel(int n, int np, int ng, float *__restrict__ s
     }
 }
 
-void quantize(const float *x, int64_t n, int64_t inp, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t,
-              hipStream_t stream) {
+// Launches the quantizer; with g and b, the LN variant (both NULL: plain quantization).
+void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const float *g, const float *b, int8_t *q,
+                 float *scales_t, int32_t *gsum_t, hipStream_t stream) {
     require(x && q && scales_t && gsum_t, "x, q, scales_t and gsum_t must not be NULL");
+    require((g == nullptr) == (b == nullptr), "LayerNorm needs both gamma and beta");
     require(n >= 0 && inp > 0 && group > 0 && inp % group == 0, "inp must be a positive multiple of group");
     require(n * inp < (1ll << 31), "activation block above 2 GiB");
     if (n == 0) return;
+    const bool ln = g != nullptr;
     const int np = (int)((n + 15) / 16 * 16), ng = (int)(inp / group);
     const unsigned blocks = (unsigned)((n + 3) / 4);
     const int ni = (int)n, ii = (int)inp, gi = (int)group;
-    const bool aligned = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (reinterpret_cast<uintptr_t>(q) % 16 == 0) &&
-                         inp % 1024 == 0;
+    auto al16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool aligned = al16(x) && al16(q) && inp % 1024 == 0 && (!ln || (al16(g) && al16(b)));
     int L = 0;
     if (aligned) {
         if (group % 1024 == 0)
@@ -146,20 +216,54 @@ void quantize(const float *x, int64_t n, int64_t inp, int64_t group, int8_t *q, 
         else if (group >= 64 && group <= 1024 && (group & (group - 1)) == 0)
             L = group / 16;
     }
+#define VX_QF(LL)                                                                                                    \
+    (ln ? quantize_fast_kernel<LL, true> : quantize_fast_kernel<LL, false>)<<<blocks, 256, 0, stream>>>(           \
+        x, ni, ii, gi, np, q, scales_t, gsum_t, g, b)
     switch (L) {
-        case 4: quantize_fast_kernel<4><<<blocks, 256, 0, stream>>>(x, ni, ii, gi, np, q, scales_t, gsum_t); break;
-        case 8: quantize_fast_kernel<8><<<blocks, 256, 0, stream>>>(x, ni, ii, gi, np, q, scales_t, gsum_t); break;
-        case 16: quantize_fast_kernel<16><<<blocks, 256, 0, stream>>>(x, ni, ii, gi, np, q, scales_t, gsum_t); break;
-        case 32: quantize_fast_kernel<32><<<blocks, 256, 0, stream>>>(x, ni, ii, gi, np, q, scales_t, gsum_t); break;
-        case 64: quantize_fast_kernel<64><<<blocks, 256, 0, stream>>>(x, ni, ii, gi, np, q, scales_t, gsum_t); break;
-        default: quantize_generic_kernel<<<blocks, 256, 0, stream>>>(x, ni, ii, gi, np, q, scales_t, gsum_t); break;
+        case 4: VX_QF(4); break;
+        case 8: VX_QF(8); break;
+        case 16: VX_QF(16); break;
+        case 32: VX_QF(32); break;
+        case 64: VX_QF(64); break;
+        default:
+            (ln ? quantize_generic_kernel<true> : quantize_generic_kernel<false>)<<<blocks, 256, 0, stream>>>(
+                x, ni, ii, gi, np, q, scales_t, gsum_t, g, b);
+            break;
     }
+#undef VX_QF
     hip_check(hipGetLastError(), "quantize kernel launch");
     if (np > n) {
         const int cnt = ng * (np - ni);
         quantize_pad_kernel<<<(cnt + 255) / 256, 256, 0, stream>>>(ni, np, ng, scales_t, gsum_t);
         hip_check(hipGetLastError(), "quantize pad kernel launch");
     }
+}
+
+void quantize(const float *x, int64_t n, int64_t inp, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t,
+              hipStream_t stream) {
+    quantize_ln(x, n, inp, group, nullptr, nullptr, q, scales_t, gsum_t, stream);
+}
+
+// LayerNorm rows to f32 (tensor.rs:700-719), one wavefront per row.
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict__ x, int n, int d,
+                                                        const float *__restrict__ g, const float *__restrict__ b,
+                                                        float *__restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= n) return;
+    const float *xr = x + (int64_t)t * d;
+    float mean, inv;
+    ln_stats(xr, d, lane, mean, inv);
+    float *yr = y + (int64_t)t * d;
+    for (int k = lane; k < d; k += 64) yr[k] = ln_apply(xr[k], mean, inv, g[k], b[k]);
+}
+
+void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y, hipStream_t stream) {
+    require(x && g && b && y, "x, gamma, beta and y must not be NULL");
+    require(n >= 0 && d > 0 && n * d < (1ll << 31), "bad LayerNorm shape");
+    if (n == 0) return;
+    layer_norm_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(x, (int)n, (int)d, g, b, y);
+    hip_check(hipGetLastError(), "layer_norm kernel launch");
 }
 
 }  // namespace vx

@@ -1,0 +1,288 @@
+"""Host-side mirror of voxrt's encoder surface on the MI355X path, over the C ABI of libvoxrt_hip.so.
+
+  TernaryLinear          crates/voxrt/src/ternary_linear.rs:30-184 (load_stacked, prepare, prepare_normed,
+                         forward_prepared_ep, forward) on device tensors, Int8 precision
+  layer_norm             tensor.rs:700-719
+  glu_dwconv_silu        encoder.rs:590-624 (the conv module between its pointwise convolutions)
+  fold_bn                encoder.rs:548-573
+  linear_f32             tensor.rs:98-127
+  Subsampling            subsampling.rs:10-204 (forward, out_frames)
+  rel_pos_table          encoder.rs:760-776
+  attention_core         encoder.rs:317-534 (attn_core_int8, all heads)
+  Encoder                GpuEncoder::{load, forward, forward_feats} (metal/mod.rs:446-603) with the CPU int8
+                         Encoder's operation order (encoder.rs:706-857); one hipGraph per frame count
+
+Device tensors are torch tensors on the current HIP device; calls are ordered on torch's current stream. Nothing
+here has a CPU fallback: every op is a HIP kernel of the library.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import kernels as K
+from .kernels import Epilogue, QuantAct, TernaryMatrix, check, lib
+
+LAYER_LINEARS = ("ff1_w1", "ff1_w2", "qkv", "o", "pos", "pw1", "pw2", "ff2_w1", "ff2_w2")
+LAYER_NORMS = ("ff1", "attn", "conv", "ff2", "out")
+
+
+def _f32(t, name):
+    import torch
+
+    return K._dev_ptr(t, torch.float32, name)
+
+
+class TernaryLinear:
+    """A ternary linear layer on the int8 path (ternary_linear.rs:30-184); weights device resident."""
+
+    def __init__(self, w: TernaryMatrix):
+        self.w = w
+
+    @classmethod
+    def load_stacked(cls, parts, group: int = 128) -> "TernaryLinear":
+        """Modules with the same input stacked along the output dimension (q|k|v): parts = [(qweight uint8
+        [out_i, ceil(inp/5)], scales_f16 uint16 [out_i, inp/group]), ...] (ternary_linear.rs:59-98)."""
+        qs = [np.ascontiguousarray(q, np.uint8) for q, _ in parts]
+        ss = [np.ascontiguousarray(np.asarray(s).view(np.uint16), np.uint16) for _, s in parts]
+        out = sum(q.shape[0] for q in qs)
+        inp = ss[0].shape[1] * group
+        if any(s.shape[1] * group != inp for s in ss) or any(q.shape[1] != (inp + 4) // 5 for q in qs):
+            raise ValueError("cannot stack, shapes differ")
+        return cls(TernaryMatrix.from_packed(np.concatenate(qs), np.concatenate(ss), out, inp, group))
+
+    @classmethod
+    def load(cls, qweight, scales_f16, group: int = 128) -> "TernaryLinear":
+        return cls.load_stacked([(qweight, scales_f16)], group)
+
+    @property
+    def out_features(self) -> int:
+        return self.w.out
+
+    @property
+    def in_features(self) -> int:
+        return self.w.inp
+
+    def prepare(self, x) -> QuantAct:
+        """Quantize an input [n, in] once (ternary_linear.rs:118-130)."""
+        return QuantAct.quantize(x, self.w.group)
+
+    def prepare_normed(self, x, gamma, beta) -> QuantAct:
+        """Fused LayerNorm -> int8 input (ternary_linear.rs:132-155)."""
+        return QuantAct.quantize_normed(x, gamma, beta, self.w.group)
+
+    def forward_prepared_ep(self, a: QuantAct, y, ep: Epilogue = Epilogue.Store) -> None:
+        K.gemm_ep(self.w, a, y, None, ep)
+
+    def forward_prepared(self, a: QuantAct, y) -> None:
+        self.forward_prepared_ep(a, y, Epilogue.Store)
+
+    def forward(self, x, y) -> None:
+        self.forward_prepared(self.prepare(x), y)
+
+
+def layer_norm(x, gamma, beta, y=None):
+    import torch
+
+    n, d = x.shape
+    y = torch.empty_like(x) if y is None else y
+    check(lib().vx_layer_norm(_f32(x, "x"), n, d, _f32(gamma, "gamma"), _f32(beta, "beta"), _f32(y, "y"),
+                              K._stream()))
+    return y
+
+
+def fold_bn(dw, gamma, beta, mean, var):
+    """HOST: BatchNorm(eval) folded into the depthwise taps: dw [d, k] -> (w_t [k, d], bias [d])."""
+    dw = np.ascontiguousarray(dw, np.float32)
+    d, k = dw.shape
+    w_t = np.empty((k, d), np.float32)
+    bias = np.empty(d, np.float32)
+    arrs = [np.ascontiguousarray(a, np.float32) for a in (gamma, beta, mean, var)]
+    check(lib().vx_fold_bn(K._np_ptr(dw), *[K._np_ptr(a) for a in arrs], d, k, K._np_ptr(w_t), K._np_ptr(bias)))
+    return w_t, bias
+
+
+def glu_dwconv_silu(g, w_t, bias, out=None):
+    """g [t, 2d] -> silu(dwconv_bn(glu(g))) [t, d]; w_t [k, d], bias [d] from fold_bn (device tensors)."""
+    import torch
+
+    t, d2 = g.shape
+    k = w_t.shape[0]
+    out = torch.empty((t, d2 // 2), dtype=torch.float32, device=g.device) if out is None else out
+    check(lib().vx_glu_dwconv_silu(_f32(g, "g"), t, d2 // 2, k, _f32(w_t, "w_t"), _f32(bias, "bias"),
+                                   _f32(out, "out"), K._stream()))
+    return out
+
+
+def linear_f32(x, w, b=None, relu=False, y=None):
+    import torch
+
+    n, in_f = x.shape
+    out_f = w.shape[0]
+    y = torch.empty((n, out_f), dtype=torch.float32, device=x.device) if y is None else y
+    check(lib().vx_linear_f32(_f32(x, "x"), n, in_f, _f32(w, "w"), _f32(b, "b"), out_f, _f32(y, "y"), int(relu),
+                              K._stream()))
+    return y
+
+
+def rel_pos_table(t: int, d: int) -> np.ndarray:
+    """HOST: [2t-1, d] relative position table (encoder.rs:760-776)."""
+    out = np.empty((2 * t - 1, d), np.float32)
+    check(lib().vx_rel_pos_table(t, d, K._np_ptr(out)))
+    return out
+
+
+def attention_ws_bytes(t: int, d: int, heads: int) -> int:
+    return int(lib().vx_attention_ws_bytes(t, d, heads))
+
+
+def attention_core(qkv, rel_k, heads, bias_u, bias_v, ctx=None, ws=None):
+    """The int8 attention core of one layer (attn_core_int8, encoder.rs:317-534): qkv [t, 3d], rel_k [2t-1, d],
+    bias_u / bias_v [heads, 128] -> ctx [t, d]."""
+    import torch
+
+    t, d3 = qkv.shape
+    d = d3 // 3
+    ctx = torch.empty((t, d), dtype=torch.float32, device=qkv.device) if ctx is None else ctx
+    nb = attention_ws_bytes(t, d, heads)
+    if nb < 0:
+        raise ValueError("attention: d must be heads * 128")
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=qkv.device) if ws is None else ws
+    scaling = float(np.float32(1.0) / np.sqrt(np.float32(d // heads)))
+    check(lib().vx_attention_core(_f32(qkv, "qkv"), _f32(rel_k, "rel_k"), t, d, heads, _f32(bias_u, "bias_u"),
+                                  _f32(bias_v, "bias_v"), scaling, C.c_void_p(ws.data_ptr()), _f32(ctx, "ctx"),
+                                  K._stream()))
+    return ctx
+
+
+SUB_KEYS = ("conv0_w", "conv0_b", "dw_w", "dw_b", "pw_w", "pw_b", "lin_w", "lin_b")
+
+
+class Subsampling:
+    """dw-striding Conv2d subsampling, 8x in time (subsampling.rs:10-204), device resident."""
+
+    def __init__(self, params: dict, n_mels: int, device):
+        import torch
+
+        self.k, self.s = int(params["k"]), int(params["s"])
+        self.c = params["conv0_b"].shape[0]
+        self.d = params["lin_b"].shape[0]
+        self.n_mels = n_mels
+        self.host = {k: np.ascontiguousarray(params[k], np.float32) for k in SUB_KEYS}
+        self.dev = {k: torch.from_numpy(v).to(device) for k, v in self.host.items()}
+
+    def out_frames(self, t: int) -> int:
+        return int(lib().vx_subsampling_frames(t, self.k, self.s))
+
+    def forward(self, feats):
+        import torch
+
+        t, nm = feats.shape
+        t3 = self.out_frames(t)
+        out = torch.empty((t3, self.d), dtype=torch.float32, device=feats.device)
+        scratch = torch.empty(int(lib().vx_subsampling_scratch_floats(t, nm, self.c, self.k, self.s)),
+                              dtype=torch.float32, device=feats.device)
+        got = C.c_int64()
+        check(lib().vx_subsampling(_f32(feats, "feats"), t, nm, self.c, self.k, self.s,
+                                   *[_f32(self.dev[k], k) for k in SUB_KEYS], self.d, _f32(scratch, "scratch"),
+                                   _f32(out, "out"), C.byref(got), K._stream()))
+        return out
+
+
+class _Config(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in ("d", "heads", "ff", "kconv", "group", "n_layers", "n_mels", "sub_channels",
+                                          "sub_kernel", "sub_stride")]
+
+
+class _LayerParams(C.Structure):
+    _fields_ = [("qweight", C.c_void_p * 9), ("scales_f16", C.c_void_p * 9), ("ln_gamma", C.c_void_p * 5),
+                ("ln_beta", C.c_void_p * 5), ("bias_u", C.c_void_p), ("bias_v", C.c_void_p), ("dw", C.c_void_p),
+                ("bn_gamma", C.c_void_p), ("bn_beta", C.c_void_p), ("bn_mean", C.c_void_p), ("bn_var", C.c_void_p)]
+
+
+class _SubParams(C.Structure):
+    _fields_ = [(k, C.c_void_p) for k in SUB_KEYS]
+
+
+class Encoder:
+    """The FastConformer encoder on one GPU, int8 path (vx_encoder_*)."""
+
+    def __init__(self, d=1024, heads=8, ff=4096, kconv=9, group=128, n_layers=24, n_mels=128, sub_channels=256,
+                 sub_kernel=3, sub_stride=2):
+        cfg = _Config(d, heads, ff, kconv, group, n_layers, n_mels, sub_channels, sub_kernel, sub_stride)
+        h = C.c_void_p()
+        check(lib().vx_encoder_create(C.byref(cfg), C.byref(h)))
+        self._h = h
+        self.d, self.heads, self.ff, self.kconv, self.group, self.n_layers = d, heads, ff, kconv, group, n_layers
+        self.n_mels, self.sub_kernel, self.sub_stride = n_mels, sub_kernel, sub_stride
+
+    def set_layer(self, i: int, p: dict) -> None:
+        """p: {"linears": {name: (qweight, scales_f16)}, "norms": {name: (g, b)}, "bias_u", "bias_v", "dw" [d, k],
+        "bn": {"gamma", "beta", "mean", "var"}} as synth.synth_layer produces (the model file's tensors)."""
+        keep = []
+
+        def ptr(a, dtype):
+            a = np.ascontiguousarray(np.asarray(a).view(dtype) if np.asarray(a).dtype != dtype and dtype == np.uint16
+                                     else a, dtype)
+            keep.append(a)
+            return a.ctypes.data
+
+        lp = _LayerParams()
+        for i_, n in enumerate(LAYER_LINEARS):
+            q, s = p["linears"][n]
+            lp.qweight[i_] = ptr(q, np.uint8)
+            lp.scales_f16[i_] = ptr(s, np.uint16)
+        for i_, n in enumerate(LAYER_NORMS):
+            g, b = p["norms"][n]
+            lp.ln_gamma[i_] = ptr(g, np.float32)
+            lp.ln_beta[i_] = ptr(b, np.float32)
+        lp.bias_u, lp.bias_v = ptr(p["bias_u"], np.float32), ptr(p["bias_v"], np.float32)
+        lp.dw = ptr(p["dw"], np.float32)
+        bn = p["bn"]
+        lp.bn_gamma, lp.bn_beta = ptr(bn["gamma"], np.float32), ptr(bn["beta"], np.float32)
+        lp.bn_mean, lp.bn_var = ptr(bn["mean"], np.float32), ptr(bn["var"], np.float32)
+        check(lib().vx_encoder_set_layer(self._h, i, C.byref(lp)))
+
+    def set_subsampling(self, params: dict) -> None:
+        arrs = {k: np.ascontiguousarray(params[k], np.float32) for k in SUB_KEYS}
+        sp = _SubParams(*[arrs[k].ctypes.data for k in SUB_KEYS])
+        check(lib().vx_encoder_set_subsampling(self._h, C.byref(sp)))
+
+    def use_graphs(self, on: bool) -> None:
+        check(lib().vx_encoder_use_graphs(self._h, int(on)))
+
+    def forward(self, x, out=None):
+        """The layer stack on x [t, d] (the subsampling output); returns out [t, d]."""
+        import torch
+
+        t = x.shape[0]
+        out = torch.empty_like(x) if out is None else out
+        check(lib().vx_encoder_forward(self._h, _f32(x, "x"), _f32(out, "out"), t, K._stream()))
+        return out
+
+    def out_frames(self, t_in: int) -> int:
+        return int(lib().vx_subsampling_frames(t_in, self.sub_kernel, self.sub_stride))
+
+    def forward_feats(self, feats, out=None):
+        """Subsampling + layers: feats [t_in, n_mels] -> [t_out, d]."""
+        import torch
+
+        t_in = feats.shape[0]
+        t3 = self.out_frames(t_in)
+        out = torch.empty((t3, self.d), dtype=torch.float32, device=feats.device) if out is None else out
+        got = C.c_int64()
+        check(lib().vx_encoder_forward_feats(self._h, _f32(feats, "feats"), t_in, _f32(out, "out"), C.byref(got),
+                                             K._stream()))
+        return out
+
+    def free(self) -> None:
+        if self._h is not None and self._h.value:
+            lib().vx_encoder_free(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

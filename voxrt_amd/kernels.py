@@ -7,6 +7,8 @@ Names, argument meaning and error behaviour follow the reference:
   QuantAct                    packed.rs:286-298     (quantize: int8 codes, scales and gsum on the device)
   gemm / gemm_ep              kernels/mod.rs:319-362
   gemm_rows_range             kernels/mod.rs:257-282
+  gemm_single                 kernels/mod.rs:285-316
+  QuantAct.quantize_normed    ternary_linear.rs:132-155 (LayerNorm fused into the quantizer)
 
 Activations and outputs are torch tensors on the current HIP device (torch is the device-memory and stream
 plumbing here); every call is ordered on torch's current stream. The HIP library must be built: nothing here falls
@@ -58,6 +60,26 @@ def lib() -> C.CDLL:
             "vx_quantize": (I, [P, I64, I64, I64, P, P, P, P]),
             "vx_gemm_ep": (I, [P, P, P, P, I64, P, P, I, F, P, P]),
             "vx_gemm_rows_range": (I, [P, P, P, P, I64, P, I64, I64, I64, I64, I, F, P]),
+            "vx_gemm_single": (I, [P, P, P, P, I64, P, P, P]),
+            "vx_quantize_normed": (I, [P, I64, I64, I64, P, P, P, P, P, P]),
+            "vx_layer_norm": (I, [P, I64, I64, P, P, P, P]),
+            "vx_glu_dwconv_silu": (I, [P, I64, I64, I64, P, P, P, P]),
+            "vx_fold_bn": (I, [P, P, P, P, P, I64, I64, P, P]),
+            "vx_linear_f32": (I, [P, I64, I64, P, P, I64, P, I, P]),
+            "vx_subsampling_frames": (I64, [I64, I64, I64]),
+            "vx_subsampling_scratch_floats": (I64, [I64, I64, I64, I64, I64]),
+            "vx_subsampling": (I, [P, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P, I64, P, P,
+                                   C.POINTER(I64), P]),
+            "vx_rel_pos_table": (I, [I64, I64, P]),
+            "vx_attention_ws_bytes": (I64, [I64, I64, I64]),
+            "vx_attention_core": (I, [P, P, I64, I64, I64, P, P, F, P, P, P]),
+            "vx_encoder_create": (I, [P, C.POINTER(P)]),
+            "vx_encoder_set_layer": (I, [P, I64, P]),
+            "vx_encoder_set_subsampling": (I, [P, P]),
+            "vx_encoder_use_graphs": (I, [P, I]),
+            "vx_encoder_forward": (I, [P, P, P, I64, P]),
+            "vx_encoder_forward_feats": (I, [P, P, I64, P, C.POINTER(I64), P]),
+            "vx_encoder_free": (None, [P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -216,6 +238,23 @@ class QuantAct:
         return self.gsum_t[:, : self.n].t()
 
     @classmethod
+    def quantize_normed(cls, x, gamma, beta, group: int, stream=None) -> "QuantAct":
+        """QuantAct::from_rows over LayerNorm rows (TernaryLinear::prepare_normed, ternary_linear.rs:132-155)."""
+        import torch
+
+        n, inp = x.shape
+        if group <= 0 or inp % group:
+            raise ValueError("inp must be a multiple of group")
+        q = torch.empty((n, inp), dtype=torch.int8, device=x.device)
+        s = torch.empty((inp // group, npad(n)), dtype=torch.float32, device=x.device)
+        g = torch.empty((inp // group, npad(n)), dtype=torch.int32, device=x.device)
+        check(lib().vx_quantize_normed(_dev_ptr(x, torch.float32, "x"), n, inp, group,
+                                       _dev_ptr(gamma, torch.float32, "gamma"), _dev_ptr(beta, torch.float32, "beta"),
+                                       _dev_ptr(q, torch.int8, "q"), _dev_ptr(s, torch.float32, "scales_t"),
+                                       _dev_ptr(g, torch.int32, "gsum_t"), _stream(stream)))
+        return cls(q, s, g, n, inp, group)
+
+    @classmethod
     def quantize(cls, x, group: int, stream=None) -> "QuantAct":
         """QuantAct::quantize_layout (packed.rs:307-436) on a float32 device tensor [n, inp]."""
         import torch
@@ -263,3 +302,14 @@ def gemm_rows_range(w: TernaryMatrix, x: QuantAct, y, r0: int, r1: int, t0: int,
                                    _dev_ptr(x.scales_t, torch.float32, "scales_t"),
                                    _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), x.n, _dev_ptr(y, torch.float32, "y"), r0,
                                    r1, t0, t1, ep.kind, ep.alpha, _stream(stream)))
+
+
+def gemm_single(w: TernaryMatrix, x: QuantAct, y, bias=None, stream=None) -> None:
+    """y[n, out] = x . w^T, then y += bias (kernels/mod.rs:285-316; the decoder's single-token GEMV)."""
+    import torch
+
+    if x.inp != w.inp or x.group != w.group:
+        raise ValueError("activation and weight shapes or groups differ")
+    check(lib().vx_gemm_single(w._h, _dev_ptr(x.x, torch.int8, "x"), _dev_ptr(x.scales_t, torch.float32, "scales_t"),
+                               _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), x.n, _dev_ptr(y, torch.float32, "y"),
+                               _dev_ptr(bias, torch.float32, "bias"), _stream(stream)))
