@@ -157,6 +157,90 @@ def cpu_baseline(gemms, budget_s=10.0):
                       f"{threads} threads, AVX-512 VNNI restatement of kernels/x86.rs with gemm_ep's block split"}
 
 
+ENC_WORKLOADS = [  # (name, log-mel frames at 10 ms, segments): 27.04 s -> T=338, 60 s -> T=750, 32 x 10 s -> T=125
+    ("t338_27s", 2704, 1),
+    ("t750_60s", 6000, 1),
+    ("b32x10s_t125", 1000, 32),
+]
+
+
+def encoder_setup(synth, n_layers=24):
+    """The 24-layer encoder with random ternary weights (synth.synth_layer) and random subsampling weights."""
+    from voxrt_amd import encoder as E
+
+    enc = E.Encoder(n_layers=n_layers)
+    params = [synth.synth_layer(i) for i in range(n_layers)]
+    for i, p in enumerate(params):
+        enc.set_layer(i, p)
+    sp = synth.synth_subsampling()
+    enc.set_subsampling(sp)
+    return enc, params, sp
+
+
+def encoder_rtfx(torch, synth, enc, dev, reps=5):
+    """Device time of encoder forwards from log-mel features (subsampling + 24 layers, each frame count replayed
+    from its hipGraph), as RTFx = audio seconds / encoder seconds."""
+    out = {}
+    for name, t_in, nseg in ENC_WORKLOADS:
+        feats = torch.from_numpy(synth.synth_normal(synth.workload_seed(4, t_in & 0xFF), t_in * 128)
+                                 .reshape(t_in, 128)).to(dev)
+        y = enc.forward_feats(feats)  # first call: workspace, graph capture
+        enc.forward_feats(feats, out=y)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            for _ in range(nseg):
+                enc.forward_feats(feats, out=y)
+        e1.record()
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) * 1e-3 / reps
+        audio = t_in * nseg / 100.0
+        out[name] = {"frames": enc.out_frames(t_in), "segments": nseg, "audio_s": audio, "ms": round(sec * 1e3, 3),
+                     "rtfx": round(audio / sec, 1)}
+    return out
+
+
+def cpu_encoder_rtfx(params, sp, synth, budget_s=30.0):
+    """The CPU int8 encoder restatement (oracle: VNNI GEMMs on all threads, glue parallel like the reference's
+    rayon loops) timed on the host cores: subsampling + 24 layers, weights unpacked and Quad16-packed beforehand
+    (load time). Stops after the budget; reports what it timed."""
+    from oracle import oracle as orc
+
+    threads = min(os.cpu_count() or 1, 16)
+    orc.set_threads(threads)
+    layers = []
+    for p in params:
+        lp = {n: (orc.unpack_rows(q, s.shape[1] * 128), orc.f16_to_f32(s)) for n, (q, s) in p["linears"].items()}
+        lp["norms"] = p["norms"]
+        lp["bias_u"], lp["bias_v"] = p["bias_u"], p["bias_v"]
+        lp["dw_t"], lp["dw_bias"] = orc.fold_bn(p["dw"], **p["bn"])
+        layers.append(orc.pack_layer_quad16(lp))
+    out = {}
+    spent = 0.0
+    for name, t_in, nseg in ENC_WORKLOADS:
+        if spent > budget_s:
+            break
+        feats = synth.synth_normal(synth.workload_seed(4, t_in & 0xFF), t_in * 128).reshape(t_in, 128)
+        t0 = time.perf_counter()
+        done = 0
+        for _ in range(nseg):
+            x = orc.subsampling(feats, sp)
+            t = x.shape[0]
+            pos = orc.rel_pos_table(t, 1024)
+            for lp in layers:
+                x = orc.conformer_layer(x, pos, lp, heads=8, threads=threads)
+            done += 1
+            if time.perf_counter() - t0 + spent > budget_s:
+                break
+        sec = (time.perf_counter() - t0) / done
+        spent += sec * done
+        out[name] = {"segments_timed": done, "ms_per_segment": round(sec * 1e3, 1),
+                     "rtfx": round(t_in / 100.0 / sec, 1)}
+    orc.set_threads(1)
+    return {"threads": threads, "kind": "port", "by_workload": out}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -164,6 +248,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-details", action="store_true")
+    ap.add_argument("--no-encoder", action="store_true", help="skip the 24-layer encoder RTFx leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the ternary GEMM path shards by "
@@ -226,12 +311,22 @@ def main():
                                "hbm_gbs": round(g.bytes / s / 1e9, 0)}
         del extra
     cpu = None if args.no_cpu else cpu_baseline(gemms)
+    if not args.no_encoder:
+        enc, eparams, esp = encoder_setup(synth)
+        details["encoder"] = encoder_rtfx(torch, synth, enc, dev)
+        enc.free()
+        if not args.no_cpu:
+            ce = cpu_encoder_rtfx(eparams, esp, synth)
+            details["encoder_cpu"] = ce
+            for k, v in ce["by_workload"].items():
+                if k in details["encoder"]:
+                    details["encoder"][k]["x_vs_cpu"] = round(details["encoder"][k]["rtfx"] / v["rtfx"], 1)
 
     line = {
         "metric": "ternary x int8 GEMM TOPS (one FastConformer layer's linear set at T=338)",
         "value": round(value, 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(gpu_s / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8 x ternary, int32 accumulate, fp32 dequant", "data": "synthetic",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "layer_linear_set_t338", "T": T, "d_model": 1024, "ffn": 4096, "group": "K",
                    "gemms": [f"{n}:{m}x{k}x{nn}" for n, m, k, nn, _, _ in layer_shapes(T)],
                    "pct_int8_peak": round(100 * value / PEAK_INT8_TOPS, 2), "wall_s": round(wall, 3)},
@@ -239,6 +334,10 @@ def main():
         "cpu_baseline": cpu,
         "details": details,
     }
+    if "encoder" in details:
+        line["config"]["encoder_rtfx_t338"] = details["encoder"]["t338_27s"]["rtfx"]
+        if "encoder_cpu" in details and "t338_27s" in details["encoder_cpu"]["by_workload"]:
+            line["config"]["encoder_cpu_rtfx_t338"] = details["encoder_cpu"]["by_workload"]["t338_27s"]["rtfx"]
     print(json.dumps(line), flush=True)
 
 

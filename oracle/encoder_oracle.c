@@ -14,6 +14,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "par.h"
 #include "voxrt_oracle.h"
 
 static inline float hsum4(const float a[4]) { return (a[0] + a[1]) + (a[2] + a[3]); } /* tensor.rs:227-229 */
@@ -58,28 +59,49 @@ static void layer_norm_row(const float *x, const float *g, const float *b, size_
     for (size_t k = 0; k < d; k++) y[k] = (x[k] - mean) * inv * g[k] + b[k];
 }
 
-/* tensor.rs:700-707 (layer_norm) */
+typedef struct {
+    const float *x, *g, *b;
+    size_t d, group;
+    float *y;
+    int8_t *q;
+    float *scales;
+    int32_t *gsum;
+} ln_ctx;
+
+static void ln_rows(void *c_, size_t lo, size_t hi) {
+    ln_ctx *c = (ln_ctx *)c_;
+    for (size_t i = lo; i < hi; i++) layer_norm_row(c->x + i * c->d, c->g, c->b, c->d, c->y + i * c->d);
+}
+
+/* tensor.rs:700-707 (layer_norm), parallel over rows as par_rows */
 void or_layer_norm(const float *x, size_t n, size_t d, const float *g, const float *b, float *y) {
-    for (size_t i = 0; i < n; i++) layer_norm_row(x + i * d, g, b, d, y + i * d);
+    ln_ctx c = {x, g, b, d, 0, y, NULL, NULL, NULL};
+    or_par_for(n, ln_rows, &c);
 }
 
 /* ternary_linear.rs:132-155 (prepare_normed, Int8) through packed.rs:315-436 (QuantAct::from_rows): each token's
  * LayerNorm row is quantized per group as it is produced. Same outputs as or_quantize. */
-void or_quantize_normed(const float *x, size_t n, size_t inp, size_t group, const float *g, const float *b,
-                        int8_t *q, float *scales, int32_t *gsum) {
-    size_t ng = inp / group;
+static void lnq_rows(void *c_, size_t lo, size_t hi) {
+    ln_ctx *c = (ln_ctx *)c_;
+    size_t inp = c->d, group = c->group, ng = inp / group;
     float *row = malloc(inp * sizeof(float));
-    for (size_t t = 0; t < n; t++) {
-        layer_norm_row(x + t * inp, g, b, inp, row);
+    for (size_t t = lo; t < hi; t++) {
+        layer_norm_row(c->x + t * inp, c->g, c->b, inp, row);
         for (size_t gi = 0; gi < ng; gi++) {
-            int8_t *dq = q + t * inp + gi * group;
-            scales[t * ng + gi] = or_quantize_group(row + gi * group, group, dq);
+            int8_t *dq = c->q + t * inp + gi * group;
+            c->scales[t * ng + gi] = or_quantize_group(row + gi * group, group, dq);
             int32_t s = 0;
-            for (size_t c = 0; c < group; c++) s += dq[c];
-            if (gsum) gsum[t * ng + gi] = s;
+            for (size_t k = 0; k < group; k++) s += dq[k];
+            if (c->gsum) c->gsum[t * ng + gi] = s;
         }
     }
     free(row);
+}
+
+void or_quantize_normed(const float *x, size_t n, size_t inp, size_t group, const float *g, const float *b,
+                        int8_t *q, float *scales, int32_t *gsum) {
+    ln_ctx c = {x, g, b, inp, group, NULL, q, scales, gsum};
+    or_par_for(n, lnq_rows, &c);
 }
 
 /* tensor.rs:810-826 (exp_row_scaled_portable): max of v*scale; v = exp_poly(v*scale - max) (two roundings);
@@ -108,9 +130,22 @@ float or_exp_row_scaled(float *row, size_t n, float scale) {
 }
 
 /* encoder.rs:592-600 with tensor.rs:936-940 (glu_row_portable): out = a * sigmoid_fast(b), a = first half. */
+typedef struct {
+    const float *a, *w, *bias;
+    size_t t, d, k;
+    float *out;
+} rows_ctx;
+
+static void glu_rows(void *c_, size_t lo, size_t hi) {
+    rows_ctx *c = (rows_ctx *)c_;
+    size_t d = c->d;
+    for (size_t i = lo; i < hi; i++)
+        for (size_t k = 0; k < d; k++) c->out[i * d + k] = c->a[i * 2 * d + k] * or_sigmoid_fast(c->a[i * 2 * d + d + k]);
+}
+
 void or_glu(const float *gbuf, size_t n, size_t d, float *out) {
-    for (size_t i = 0; i < n; i++)
-        for (size_t c = 0; c < d; c++) out[i * d + c] = gbuf[i * 2 * d + c] * or_sigmoid_fast(gbuf[i * 2 * d + d + c]);
+    rows_ctx c = {gbuf, NULL, NULL, n, d, 0, out};
+    or_par_for(n, glu_rows, &c);
 }
 
 /* encoder.rs:548-573 (ConvModule::load): BatchNorm(eval) folded into the depthwise taps, tap-major [k][d]:
@@ -126,10 +161,12 @@ void or_fold_bn(const float *dw, const float *gamma, const float *beta, const fl
 
 /* encoder.rs:602-624: row i = bias, + w[kk] * a[i + kk - pad] for each tap in order (unfused, taps outside
  * [0, t) skipped), then silu_fast per element (tensor.rs:962-973). */
-void or_dwconv_bn_silu(const float *a, size_t t, size_t d, size_t k, const float *dw_t, const float *dw_bias,
-                       float *out) {
-    size_t pad = (k - 1) / 2;
-    for (size_t i = 0; i < t; i++) {
+static void dwconv_rows(void *c_, size_t lo, size_t hi) {
+    rows_ctx *c = (rows_ctx *)c_;
+    const float *a = c->a, *dw_t = c->w, *dw_bias = c->bias;
+    size_t t = c->t, d = c->d, k = c->k, pad = (k - 1) / 2;
+    float *out = c->out;
+    for (size_t i = lo; i < hi; i++) {
         float *row = out + i * d;
         memcpy(row, dw_bias, d * sizeof(float));
         for (size_t kk = 0; kk < k; kk++) {
@@ -141,6 +178,12 @@ void or_dwconv_bn_silu(const float *a, size_t t, size_t d, size_t k, const float
         }
         for (size_t c = 0; c < d; c++) row[c] = or_silu_fast(row[c]);
     }
+}
+
+void or_dwconv_bn_silu(const float *a, size_t t, size_t d, size_t k, const float *dw_t, const float *dw_bias,
+                       float *out) {
+    rows_ctx c = {a, dw_t, dw_bias, t, d, k, out};
+    or_par_for(t, dwconv_rows, &c);
 }
 
 /* encoder.rs:760-776 (rel_pos_table): [2t-1][d], positions t-1 .. -(t-1), (sin, cos) interleaved per frequency,
@@ -189,6 +232,14 @@ static float dot_lanes8(const float *x, const float *w, size_t n) {
     return r;
 }
 
+typedef struct {
+    const float *x, *w, *b;
+    size_t in_f, out_f;
+    float *y;
+} lin_ctx;
+
+static void linear_rows(void *c_, size_t lo, size_t hi);
+
 /* tensor.rs:98-127 (linear): one token -> gemv_portable (tensor.rs:284-303: 4-row blocks by dot_lanes8, the
  * leftover rows by dot); otherwise tile_rows_portable (tensor.rs:233-261) for every token: four fused lanes over
  * 4-column steps, the tail unfused, y = (hsum4 + tail) + bias. */
@@ -202,8 +253,17 @@ void or_linear_f32(const float *x, size_t n, size_t in_f, const float *w, const 
         }
         return;
     }
+    lin_ctx lc = {x, w, b, in_f, out_f, y};
+    or_par_for(n, linear_rows, &lc);
+}
+
+static void linear_rows(void *c_, size_t lo, size_t hi) {
+    lin_ctx *lc = (lin_ctx *)c_;
+    const float *x = lc->x, *w = lc->w, *b = lc->b;
+    size_t in_f = lc->in_f, out_f = lc->out_f;
+    float *y = lc->y;
     size_t c4 = in_f / 4 * 4;
-    for (size_t tk = 0; tk < n; tk++) {
+    for (size_t tk = lo; tk < hi; tk++) {
         const float *xr = x + tk * in_f;
         for (size_t o = 0; o < out_f; o++) {
             const float *wr = w + o * in_f;
@@ -226,6 +286,57 @@ size_t or_subsampling_frames(size_t t, size_t k, size_t s) {
     return n;
 }
 
+typedef struct {
+    const float *in, *w, *b;
+    size_t tin, fin, c, k, s, p, tout, fout;
+    float *out;
+} conv_ctx;
+
+/* stage 0 rows [lo, hi) of the output time axis */
+static void conv0_rows(void *c_, size_t lo, size_t hi) {
+    conv_ctx *q = (conv_ctx *)c_;
+    size_t c = q->c, k = q->k, s = q->s, p = q->p;
+    for (size_t ot = lo; ot < hi; ot++)
+        for (size_t of = 0; of < q->fout; of++) {
+            float *o = q->out + (ot * q->fout + of) * c;
+            memcpy(o, q->b, c * sizeof(float));
+            for (size_t kt = 0; kt < k; kt++) {
+                int64_t it = (int64_t)(ot * s + kt) - (int64_t)p;
+                if (it < 0 || it >= (int64_t)q->tin) continue;
+                for (size_t kf = 0; kf < k; kf++) {
+                    int64_t i_f = (int64_t)(of * s + kf) - (int64_t)p;
+                    if (i_f < 0 || i_f >= (int64_t)q->fin) continue;
+                    float v = q->in[(size_t)it * q->fin + (size_t)i_f];
+                    const float *wt = q->w + (kt * k + kf) * c;
+                    for (size_t ch = 0; ch < c; ch++) o[ch] += wt[ch] * v;
+                }
+            }
+            for (size_t ch = 0; ch < c; ch++) o[ch] = o[ch] > 0.0f ? o[ch] : 0.0f;
+        }
+}
+
+/* depthwise stage rows [lo, hi) */
+static void dw_rows(void *c_, size_t lo, size_t hi) {
+    conv_ctx *q = (conv_ctx *)c_;
+    size_t c = q->c, k = q->k, s = q->s, p = q->p;
+    for (size_t ot = lo; ot < hi; ot++)
+        for (size_t of = 0; of < q->fout; of++) {
+            float *o = q->out + (ot * q->fout + of) * c;
+            memcpy(o, q->b, c * sizeof(float));
+            for (size_t kt = 0; kt < k; kt++) {
+                int64_t it = (int64_t)(ot * s + kt) - (int64_t)p;
+                if (it < 0 || it >= (int64_t)q->tin) continue;
+                for (size_t kf = 0; kf < k; kf++) {
+                    int64_t i_f = (int64_t)(of * s + kf) - (int64_t)p;
+                    if (i_f < 0 || i_f >= (int64_t)q->fin) continue;
+                    const float *xi = q->in + ((size_t)it * q->fin + (size_t)i_f) * c;
+                    const float *wt = q->w + (kt * k + kf) * c;
+                    for (size_t ch = 0; ch < c; ch++) o[ch] += wt[ch] * xi[ch];
+                }
+            }
+        }
+}
+
 /* subsampling.rs:124-204 (Subsampling::forward), channels-last [T, F, C]:
  *   stage 0: 3x3 stride-s conv 1 -> C (bias first, taps kt-major then kf, unfused), ReLU;
  *   two stages of depthwise 3x3 stride-s (no activation), pointwise C -> C by the f32 linear (+ bias), ReLU;
@@ -238,44 +349,15 @@ size_t or_subsampling(const float *feats, size_t t, size_t n_mels, size_t c, siz
     size_t p = (k - 1) / 2;
     size_t t1 = out_len(t, k, s, p), f1 = out_len(n_mels, k, s, p);
     float *x = calloc(t1 * f1 * c, sizeof(float));
-    for (size_t ot = 0; ot < t1; ot++)
-        for (size_t of = 0; of < f1; of++) {
-            float *o = x + (ot * f1 + of) * c;
-            memcpy(o, conv0_b, c * sizeof(float));
-            for (size_t kt = 0; kt < k; kt++) {
-                int64_t it = (int64_t)(ot * s + kt) - (int64_t)p;
-                if (it < 0 || it >= (int64_t)t) continue;
-                for (size_t kf = 0; kf < k; kf++) {
-                    int64_t i_f = (int64_t)(of * s + kf) - (int64_t)p;
-                    if (i_f < 0 || i_f >= (int64_t)n_mels) continue;
-                    float v = feats[(size_t)it * n_mels + (size_t)i_f];
-                    const float *wt = conv0_w + (kt * k + kf) * c;
-                    for (size_t ch = 0; ch < c; ch++) o[ch] += wt[ch] * v;
-                }
-            }
-            for (size_t ch = 0; ch < c; ch++) o[ch] = o[ch] > 0.0f ? o[ch] : 0.0f;
-        }
+    conv_ctx cc0 = {feats, conv0_w, conv0_b, t, n_mels, c, k, s, p, t1, f1, x};
+    or_par_for(t1, conv0_rows, &cc0);
     size_t tc = t1, fc = f1;
     for (int stage = 0; stage < 2; stage++) {
         size_t t2 = out_len(tc, k, s, p), f2 = out_len(fc, k, s, p);
         const float *w = dw_w + (size_t)stage * k * k * c, *b = dw_b + (size_t)stage * c;
         float *y = calloc(t2 * f2 * c, sizeof(float));
-        for (size_t ot = 0; ot < t2; ot++)
-            for (size_t of = 0; of < f2; of++) {
-                float *o = y + (ot * f2 + of) * c;
-                memcpy(o, b, c * sizeof(float));
-                for (size_t kt = 0; kt < k; kt++) {
-                    int64_t it = (int64_t)(ot * s + kt) - (int64_t)p;
-                    if (it < 0 || it >= (int64_t)tc) continue;
-                    for (size_t kf = 0; kf < k; kf++) {
-                        int64_t i_f = (int64_t)(of * s + kf) - (int64_t)p;
-                        if (i_f < 0 || i_f >= (int64_t)fc) continue;
-                        const float *xi = x + ((size_t)it * fc + (size_t)i_f) * c;
-                        const float *wt = w + (kt * k + kf) * c;
-                        for (size_t ch = 0; ch < c; ch++) o[ch] += wt[ch] * xi[ch];
-                    }
-                }
-            }
+        conv_ctx cd = {x, w, b, tc, fc, c, k, s, p, t2, f2, y};
+        or_par_for(t2, dw_rows, &cd);
         size_t n_pos = t2 * f2;
         float *z = malloc(n_pos * c * sizeof(float));
         or_linear_f32(y, n_pos, c, pw_w + (size_t)stage * c * c, pw_b + (size_t)stage * c, c, z);
@@ -299,23 +381,26 @@ static int32_t idot(const int8_t *a, const int8_t *b, size_t n) {
     return s;
 }
 
-/* encoder.rs:317-534 (attn_core_int8) for all heads. qkv [t][3d] (q | k | v), rel_k [2t-1][d]; ctx [t][d].
- * Per head: q + bias_u and q + bias_v quantized per token (one group = dh), keys [t2][dh], relative positions
- * [np2][dh] and vT [dh][t16] quantized per row (one group each; rows past the end are zero); the content score
- * S1[i][j] and the position score S2[i][p] are single-group int8 GEMM outputs fma((float)S, xs * ws, 0)
- * (kernels/mod.rs:166-210); score = S1[i][j] + S2[i][t-1-i+j]; exp_row_scaled with `scaling`; the row of
- * exponentials, zero-padded to t16, is quantized in one group and its scale multiplied by 1/sum; ctx is the
- * single-group int8 GEMM of those probabilities with vT. */
-void or_attn_core_int8(const float *qkv, const float *rel_k, size_t t, size_t d, size_t h, const float *bias_u,
-                       const float *bias_v, float scaling, float *ctx) {
+typedef struct {
+    const float *qkv, *rel_k, *bias_u, *bias_v;
+    size_t t, d, h;
+    float scaling;
+    float *ctx;
+} attn_ctx;
+
+static void attn_heads(void *c_, size_t lo, size_t hi) {
+    attn_ctx *A = (attn_ctx *)c_;
+    const float *qkv = A->qkv, *rel_k = A->rel_k;
+    size_t t = A->t, d = A->d, h = A->h;
+    float *ctx = A->ctx;
     size_t dh = d / h, np = 2 * t - 1, t2 = (t + 1) / 2 * 2, np2 = (np + 1) / 2 * 2, t16 = (t + 15) / 16 * 16;
     size_t d3 = 3 * d;
     int8_t *qu = malloc(t * dh), *qv = malloc(t * dh), *kq = malloc(t2 * dh), *rq = malloc(np2 * dh);
     int8_t *vq = malloc(dh * t16), *pq = malloc(t16);
     float *qus = malloc(t * 4), *qvs = malloc(t * 4), *ks = malloc(t2 * 4), *rs = malloc(np2 * 4), *vs = malloc(dh * 4);
     float *tmp = malloc((t16 > dh ? t16 : dh) * sizeof(float)), *row = malloc(t16 * sizeof(float));
-    for (size_t head = 0; head < h; head++) {
-        const float *bu = bias_u + head * dh, *bv = bias_v + head * dh;
+    for (size_t head = lo; head < hi; head++) {
+        const float *bu = A->bias_u + head * dh, *bv = A->bias_v + head * dh;
         for (size_t i = 0; i < t; i++) {
             const float *qi = qkv + i * d3 + head * dh;
             for (size_t c = 0; c < dh; c++) tmp[c] = qi[c] + bu[c];
@@ -348,7 +433,7 @@ void or_attn_core_int8(const float *qkv, const float *rel_k, size_t t, size_t d,
                 float s2 = fmaf((float)idot(qv + i * dh, rq + p * dh, dh), qvs[i] * rs[p], 0.0f);
                 row[j] = s1 + s2;
             }
-            float inv = 1.0f / or_exp_row_scaled(row, t, scaling);
+            float inv = 1.0f / or_exp_row_scaled(row, t, A->scaling);
             for (size_t j = t; j < t16; j++) row[j] = 0.0f;
             float ps = or_quantize_group(row, t16, pq);
             ps = ps * inv;
@@ -358,6 +443,19 @@ void or_attn_core_int8(const float *qkv, const float *rel_k, size_t t, size_t d,
     }
     free(qu); free(qv); free(kq); free(rq); free(vq); free(pq);
     free(qus); free(qvs); free(ks); free(rs); free(vs); free(tmp); free(row);
+}
+
+/* encoder.rs:317-534 (attn_core_int8) for all heads. qkv [t][3d] (q | k | v), rel_k [2t-1][d]; ctx [t][d].
+ * Per head: q + bias_u and q + bias_v quantized per token (one group = dh), keys [t2][dh], relative positions
+ * [np2][dh] and vT [dh][t16] quantized per row (one group each; rows past the end are zero); the content score
+ * S1[i][j] and the position score S2[i][p] are single-group int8 GEMM outputs fma((float)S, xs * ws, 0)
+ * (kernels/mod.rs:166-210); score = S1[i][j] + S2[i][t-1-i+j]; exp_row_scaled with `scaling`; the row of
+ * exponentials, zero-padded to t16, is quantized in one group and its scale multiplied by 1/sum; ctx is the
+ * single-group int8 GEMM of those probabilities with vT. Heads run in parallel. */
+void or_attn_core_int8(const float *qkv, const float *rel_k, size_t t, size_t d, size_t h, const float *bias_u,
+                       const float *bias_v, float scaling, float *ctx) {
+    attn_ctx A = {qkv, rel_k, bias_u, bias_v, t, d, h, scaling, ctx};
+    or_par_for(h, attn_heads, &A);
 }
 
 /* ------------------------------------------------------------------------------------------ encoder (int8) */
@@ -370,9 +468,11 @@ typedef struct {
     size_t out, inp, group;
     int8_t *wq;
     float *sq;
+    int own;
 } tlin;
 
-static void tlin_init(tlin *l, const int8_t *w, const float *ws, size_t out, size_t inp, size_t group) {
+static void tlin_init(tlin *l, const int8_t *w, const float *ws, size_t out, size_t inp, size_t group,
+                      const int8_t *wq_pre, const float *sq_pre) {
     l->w = w;
     l->ws = ws;
     l->out = out;
@@ -380,7 +480,14 @@ static void tlin_init(tlin *l, const int8_t *w, const float *ws, size_t out, siz
     l->group = group;
     l->wq = NULL;
     l->sq = NULL;
+    l->own = 0;
+    if (wq_pre && sq_pre && or_have_vnni()) { /* packed at load time, as TernaryLinear::load does */
+        l->wq = (int8_t *)wq_pre;
+        l->sq = (float *)sq_pre;
+        return;
+    }
     if (or_have_vnni()) {
+        l->own = 1;
         l->wq = malloc(or_quad16_bytes(out, inp));
         l->sq = malloc((out + 15) / 16 * 16 * (inp / group) * sizeof(float));
         or_quad16_pack(w, out, inp, group, ws, l->wq, l->sq);
@@ -388,8 +495,10 @@ static void tlin_init(tlin *l, const int8_t *w, const float *ws, size_t out, siz
 }
 
 static void tlin_free(tlin *l) {
-    free(l->wq);
-    free(l->sq);
+    if (l->own) {
+        free(l->wq);
+        free(l->sq);
+    }
 }
 
 typedef struct {
@@ -427,8 +536,9 @@ static void tlin_gemm(const tlin *l, const qact *a, float *y, int ep, float alph
  *   9..17  their scales f32 [out][inp/group], same order
  *   18..27 LayerNorm (g, b) of norm_feed_forward1, norm_self_att, norm_conv, norm_feed_forward2, norm_out
  *   28, 29 bias_u, bias_v [heads][dh]
- *   30, 31 depthwise taps [k][d] and bias [d] with BatchNorm folded (or_fold_bn) */
-enum { P_W = 0, P_S = 9, P_LN = 18, P_BU = 28, P_BV = 29, P_DW = 30, P_DWB = 31, P_COUNT = 32 };
+ *   30, 31 depthwise taps [k][d] and bias [d] with BatchNorm folded (or_fold_bn)
+ *   32..49 optional (NULL: packed per call) Quad16 weights and scales of the 9 linears (or_quad16_pack), as pairs */
+enum { P_W = 0, P_S = 9, P_LN = 18, P_BU = 28, P_BV = 29, P_DW = 30, P_DWB = 31, P_Q16 = 32, P_COUNT = 50 };
 
 /* encoder.rs:706-756 (ConformerLayer::forward_profiled), int8 path, in place on x [t][d]:
  *   x += 0.5 * ff1.w2(quant(silu(ff1.w1(ln_quant(x)))))            (encoder.rs:79-94)
@@ -449,7 +559,8 @@ void or_conformer_layer(float *x, size_t t, const float *pos_emb, const void *co
     size_t outs[9] = {ff, d, 3 * d, d, d, 2 * d, d, ff, d}, inps[9] = {d, ff, d, d, d, d, d, d, ff};
     tlin L[9];
     for (int i = 0; i < 9; i++)
-        tlin_init(&L[i], (const int8_t *)p[P_W + i], (const float *)p[P_S + i], outs[i], inps[i], group);
+        tlin_init(&L[i], (const int8_t *)p[P_W + i], (const float *)p[P_S + i], outs[i], inps[i], group,
+                  (const int8_t *)p[P_Q16 + 2 * i], (const float *)p[P_Q16 + 2 * i + 1]);
     const float *ln_g[5], *ln_b[5];
     for (int i = 0; i < 5; i++) {
         ln_g[i] = (const float *)p[P_LN + 2 * i];

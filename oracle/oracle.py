@@ -52,6 +52,8 @@ def lib() -> C.CDLL:
             "or_quad16_pack": (None, [P, S, S, S, P, P, P]),
             "or_gemm_vnni_range": (None, [P, P, S, S, S, P, P, P, S, P, S, S, S, S, I, F]),
             "or_gemm_ep_vnni": (None, [P, P, S, S, S, P, P, P, S, P, I, F, I, S]),
+            "or_get_threads": (I, []),
+            "or_set_threads": (None, [I]),
             "or_row_mean_var": (None, [P, S, P, P]),
             "or_layer_norm": (None, [P, S, S, P, P, P]),
             "or_quantize_normed": (None, [P, S, S, S, P, P, P, P, P]),
@@ -293,8 +295,27 @@ def conformer_layer(x, pos_emb, lp, heads, kconv=9, group=128, threads=None):
     for n in LAYER_NORMS:
         keep += [_f32(lp["norms"][n][0]), _f32(lp["norms"][n][1])]
     keep += [_f32(lp["bias_u"]), _f32(lp["bias_v"]), _f32(lp["dw_t"]), _f32(lp["dw_bias"])]
-    ptrs = (C.c_void_p * len(keep))(*[a.ctypes.data for a in keep])
+    addrs = [a.ctypes.data for a in keep]
+    q16 = lp.get("quad16")  # {name: (wq, sq)} packed once (pack_layer_quad16), else packed per call
+    for n in LAYER_LINEARS:
+        if q16 is not None:
+            keep += [q16[n][0], q16[n][1]]
+            addrs += [q16[n][0].ctypes.data, q16[n][1].ctypes.data]
+        else:
+            addrs += [None, None]
+    ptrs = (C.c_void_p * len(addrs))(*addrs)
     pos_emb = _f32(pos_emb)
     lib().or_conformer_layer(_p(x), t, _p(pos_emb), ptrs, d, heads, ff, kconv, group,
                              threads or os.cpu_count() or 1)
     return x
+
+
+def set_threads(n: int) -> None:
+    """Thread count of the oracle's parallel loops (results are the same for any count)."""
+    lib().or_set_threads(int(n))
+
+
+def pack_layer_quad16(lp, group=128):
+    """Quad16 copies of a layer's 9 linears for the VNNI GEMM (TernaryLinear::load's repack), done once."""
+    lp["quad16"] = {n: quad16_pack(lp[n][0], lp[n][1], group) for n in LAYER_LINEARS}
+    return lp

@@ -5,6 +5,7 @@
  * Rust reference performs it (Rust never contracts a*b+c; `mul_add` is a correctly rounded fma, as is C's fmaf).
  */
 #include "voxrt_oracle.h"
+#include "par.h"
 
 #include <math.h>
 #include <pthread.h>
@@ -133,18 +134,74 @@ float or_quantize_group(const float *src, size_t n, int8_t *dst) {
 
 /* packed.rs:307-436 (QuantAct::quantize_layout, Rows/Quad16) — per (token, group) scale and codes, plus the code
  * sums `gsum` (packed.rs:349-360). q has n rows of inp bytes; scales and gsum are [n, inp/group]. */
-void or_quantize(const float *x, size_t n, size_t inp, size_t group, int8_t *q, float *scales, int32_t *gsum) {
-    size_t ng = inp / group;
-    for (size_t t = 0; t < n; t++)
+/* ---- parallel-for (par.h) */
+static int g_threads = 1;
+int or_get_threads(void) { return g_threads; }
+void or_set_threads(int n) { g_threads = n < 1 ? 1 : (n > 256 ? 256 : n); }
+
+typedef struct {
+    or_range_fn fn;
+    void *ctx;
+    size_t lo, hi;
+} par_job;
+
+static void *par_main(void *p) {
+    par_job *j = (par_job *)p;
+    j->fn(j->ctx, j->lo, j->hi);
+    return NULL;
+}
+
+void or_par_for(size_t n, or_range_fn fn, void *ctx) {
+    size_t T = (size_t)g_threads;
+    if (T > n) T = n;
+    if (T <= 1) {
+        if (n) fn(ctx, 0, n);
+        return;
+    }
+    pthread_t th[256];
+    par_job jobs[256];
+    size_t chunk = (n + T - 1) / T;
+    size_t used = 0;
+    for (size_t i = 0; i < T; i++) {
+        size_t lo = i * chunk, hi = lo + chunk < n ? lo + chunk : n;
+        if (lo >= hi) break;
+        jobs[i] = (par_job){fn, ctx, lo, hi};
+        if (pthread_create(&th[i], NULL, par_main, &jobs[i]) != 0) { /* fall back to running inline */
+            fn(ctx, lo, hi);
+            th[i] = 0;
+        }
+        used = i + 1;
+    }
+    for (size_t i = 0; i < used; i++)
+        if (th[i]) pthread_join(th[i], NULL);
+}
+
+typedef struct {
+    const float *x;
+    size_t inp, group;
+    int8_t *q;
+    float *scales;
+    int32_t *gsum;
+} quant_ctx;
+
+static void quantize_rows(void *c_, size_t lo, size_t hi) {
+    quant_ctx *c = (quant_ctx *)c_;
+    size_t inp = c->inp, group = c->group, ng = inp / group;
+    for (size_t t = lo; t < hi; t++)
         for (size_t g = 0; g < ng; g++) {
-            int8_t *d = q + t * inp + g * group;
-            scales[t * ng + g] = or_quantize_group(x + t * inp + g * group, group, d);
-            if (gsum) {
+            int8_t *d = c->q + t * inp + g * group;
+            c->scales[t * ng + g] = or_quantize_group(c->x + t * inp + g * group, group, d);
+            if (c->gsum) {
                 int32_t s = 0;
-                for (size_t c = 0; c < group; c++) s += d[c];
-                gsum[t * ng + g] = s;
+                for (size_t k = 0; k < group; k++) s += d[k];
+                c->gsum[t * ng + g] = s;
             }
         }
+}
+
+void or_quantize(const float *x, size_t n, size_t inp, size_t group, int8_t *q, float *scales, int32_t *gsum) {
+    quant_ctx c = {x, inp, group, q, scales, gsum};
+    or_par_for(n, quantize_rows, &c);
 }
 
 /* tensor.rs:829-848 exp_poly — clamp to [-87, 88], n = round_half_even(x*log2 e), two-step Cody-Waite reduction

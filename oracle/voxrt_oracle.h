@@ -78,6 +78,10 @@ void or_gemm_ep_vnni(const int8_t *wq, const float *scales_q, size_t out, size_t
                      const int8_t *x, const float *xs, const int32_t *gsum, size_t n, float *y, int ep, float alpha,
                      int threads, size_t blocks_mult);
 
+/* Thread count of the oracle's parallel loops (default 1; results do not depend on it). */
+int or_get_threads(void);
+void or_set_threads(int n);
+
 /* Encoder side (encoder_oracle.c) */
 void or_row_mean_var(const float *x, size_t d, float *mean, float *var);
 void or_layer_norm(const float *x, size_t n, size_t d, const float *g, const float *b, float *y);

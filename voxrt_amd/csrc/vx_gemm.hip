@@ -682,6 +682,175 @@ __global__ __launch_bounds__(256) void tgemm_splitk_kernel(const GemmArgs a) {
 }
 
 
+// Split-K over groups (several groups, G = 64 * SPG): chunk c of the K dimension holds groups 4c .. 4c+3 and wave w
+// computes group 4c + w, its MFMA chain seeded with the group's -sum(x codes) so it ends at S_g. After every chunk
+// the four group sums of each output meet in LDS and are folded in ascending group order into the fp32
+// accumulators, acc = fma((float)S_g, xs[t][g] * ws[o][g], acc) — the reference's fold, so the result is the
+// scalar kernel's bit for bit. Small-M shapes get 4x the wavefronts of the one-wave-per-tile kernels this way.
+template <int MT, int NT, bool TERN, bool GS, int SPG, int D>
+__global__ __launch_bounds__(256) void tgemm_splitk_groups_kernel(const GemmArgs a) {
+    constexpr int BM = 16 * MT, BN = 16 * NT, BNP = BN + 4;
+    static_assert(BM * BN == 256 * 8, "each thread folds 8 outputs");
+    static_assert(D % SPG == 0, "the ring depth covers whole groups");
+    __shared__ __attribute__((aligned(16))) int red[4][BM * BNP];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int arow = lane & 15, aj = lane >> 4;
+    const int m0 = (int)a.m_base + (int)blockIdx.y * BM;
+    const int n0 = (int)a.n_base + (int)blockIdx.x * BN;
+    const int inp = (int)a.inp, nk = inp / 64, ng = (int)a.ng, nchunk = ng / 4, nsw = nchunk * SPG;
+    const int np = (int)a.np;
+
+    const auto xrs = make_rsrc(a.xq, a.xq_bytes);
+    const auto wrs = make_rsrc(a.w, a.w_bytes);
+    const auto srs = make_rsrc(a.xs, a.xs_bytes);
+    const auto grs = make_rsrc(a.xg, a.xs_bytes);
+    const auto wsrs = make_rsrc(a.ws_t, a.ws_bytes);
+
+    int va[MT];
+#pragma unroll
+    for (int mb = 0; mb < MT; mb++) va[mb] = (m0 + mb * 16 + arow) * inp + 16 * aj;
+    constexpr int BBYTES = TERN ? 4 : 16;
+    const int vb = lane * BBYTES;
+
+    typedef typename std::conditional<TERN, uint32_t, v4i>::type BReg;
+    v4i ra[D][MT];
+    BReg rb[D][NT];
+    // this wave's k-step s lies in chunk s / SPG: global step ((s / SPG) * 4 + wave) * SPG + s % SPG
+    auto kb_of = [&](int st) { return ((st / SPG) * 4 + wave) * SPG + st % SPG; };
+    auto issue = [&](int st, int slot) {
+        const int kb = kb_of(st);
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++) ra[slot][mb] = __builtin_amdgcn_raw_buffer_load_b128(xrs, va[mb], kb * 64, 0);
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++) {
+            const int soff = ((n0 / 16 + nb) * nk + kb) * 64 * BBYTES;
+            if constexpr (TERN)
+                rb[slot][nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, vb, soff, 0);
+            else
+                rb[slot][nb] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vb, soff, 0);
+        }
+    };
+
+    // fold state: thread -> token tt of the tile, rows c0 .. c0+7
+    const int tt = tid / (BN / 8), c0 = (tid % (BN / 8)) * 8;
+    const int t = m0 + tt, o0 = n0 + c0;
+    float accf[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) accf[j] = 0.0f;
+
+    v4i acc[MT][NT];
+    auto compute = [&](int slot, int st) {
+        v4i bv[NT];
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++) {
+            if constexpr (TERN)
+                bv[nb] = widen_codes(rb[slot][nb]);
+            else
+                bv[nb] = rb[slot][nb];
+        }
+        if (st % SPG == 0) {  // first step of a group: seed with -gsum of the group (ternary) or zero
+            const int g = (st / SPG) * 4 + wave;
+#pragma unroll
+            for (int mb = 0; mb < MT; mb++) {
+                v4i c = v4i{0, 0, 0, 0};
+                if constexpr (TERN)
+                    c = -(v4i)__builtin_amdgcn_raw_buffer_load_b128(grs, (g * np + m0 + mb * 16 + 4 * aj) * 4, 0, 0);
+#pragma unroll
+                for (int nb = 0; nb < NT; nb++)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ra[slot][mb], bv[nb], c, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+                for (int nb = 0; nb < NT; nb++)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ra[slot][mb], bv[nb], acc[mb][nb], 0, 0, 0);
+        }
+        if (st % SPG == SPG - 1) {  // group complete: the chunk's four group sums meet in LDS, then the fold
+#pragma unroll
+            for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+                for (int nb = 0; nb < NT; nb++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        red[wave][(mb * 16 + 4 * aj + e) * BNP + nb * 16 + arow] = acc[mb][nb][e];
+            __syncthreads();
+            const int chunk = st / SPG;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const int g = chunk * 4 + w;
+                const v4i lo = *(const v4i *)&red[w][tt * BNP + c0];
+                const v4i hi = *(const v4i *)&red[w][tt * BNP + c0 + 4];
+                const float xs = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, (g * np + t) * 4, 0, 0));
+                const v4i wlo = __builtin_amdgcn_raw_buffer_load_b128(wsrs, (g * (int)a.out_pad + o0) * 4, 0, 0);
+                const v4i whi = __builtin_amdgcn_raw_buffer_load_b128(wsrs, (g * (int)a.out_pad + o0) * 4 + 16, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    accf[j] = __builtin_fmaf((float)lo[j], xs * __int_as_float(wlo[j]), accf[j]);
+                    accf[4 + j] = __builtin_fmaf((float)hi[j], xs * __int_as_float(whi[j]), accf[4 + j]);
+                }
+                if constexpr (GS) {
+                    if (t >= a.t0 && t < a.t1)
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            const int o = o0 + j;
+                            if (o >= a.r0 && o < a.r1) a.gs[((int64_t)g * a.n + t) * a.out + o] = j < 4 ? lo[j] : hi[j - 4];
+                        }
+                }
+            }
+            __syncthreads();
+        }
+    };
+
+    // D divides nsw and is a multiple of SPG (the host picks it): prologue, steady state, drain
+#pragma unroll
+    for (int i = 0; i < D; i++) issue(i, i);
+    for (int s0 = 0; s0 < nsw - D; s0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; i++) {
+            compute(i, s0 + i);
+            issue(s0 + i + D, i);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < D; i++) compute(i, nsw - D + i);
+
+    if (t < a.t0 || t >= a.t1) return;
+    const float *v = accf;
+    float *yrow = a.y + (int64_t)t * a.out;
+    if (a.vec_ok && o0 >= a.r0 && o0 + 8 <= a.r1) {
+        float old[8] = {0, 0, 0, 0, 0, 0, 0, 0}, bia[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (a.ep == VX_EP_ADD_SCALED) {
+            const float4 p = *(const float4 *)(yrow + o0), q = *(const float4 *)(yrow + o0 + 4);
+            old[0] = p.x, old[1] = p.y, old[2] = p.z, old[3] = p.w, old[4] = q.x, old[5] = q.y, old[6] = q.z,
+            old[7] = q.w;
+        }
+        if (a.bias) {
+            const float4 p = *(const float4 *)(a.bias + o0), q = *(const float4 *)(a.bias + o0 + 4);
+            bia[0] = p.x, bia[1] = p.y, bia[2] = p.z, bia[3] = p.w, bia[4] = q.x, bia[5] = q.y, bia[6] = q.z,
+            bia[7] = q.w;
+        }
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            r[j] = ep_apply(a.ep, a.alpha, old[j], v[j]);
+            if (a.bias) r[j] = r[j] + bia[j];
+        }
+        *(float4 *)(yrow + o0) = make_float4(r[0], r[1], r[2], r[3]);
+        *(float4 *)(yrow + o0 + 4) = make_float4(r[4], r[5], r[6], r[7]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int o = o0 + j;
+            if (o < a.r0 || o >= a.r1) continue;
+            float r = ep_apply(a.ep, a.alpha, a.ep == VX_EP_ADD_SCALED ? yrow[o] : 0.0f, v[j]);
+            if (a.bias) r = r + a.bias[o];
+            yrow[o] = r;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Large-token kernel (one group, G = K; K a multiple of 512). Built for MFMA throughput:
 //  * v_mfma_i32_32x32x32_i8: a wavefront owns a 128 x 64 output tile (4 x 2 blocks of 32 x 32, 128 int32
@@ -971,7 +1140,7 @@ void launch_lds(const GemmArgs &a, bool single, int d, hipStream_t st) {
     }
 }
 
-enum Kind { kDirect, kSplitK, kLds, kBig };
+enum Kind { kDirect, kSplitK, kLds, kBig, kSplitG };
 
 struct Plan {
     Kind kind;
@@ -991,8 +1160,10 @@ Plan plan_for(const GemmArgs &a, bool tern, bool gs, bool single) {
     const bool splitk_ok = single && (a.inp / 64) % 4 == 0;
     const bool lds_fast_ok = tern && !gs && (a.inp / 64) % 8 == 0;
     const bool big_ok = tern && single && !gs && (a.inp / 64) % 8 == 0 && a.y_bytes != 0;
+    const bool splitg_ok = !single && a.spg == 2 && a.ng % 4 == 0;
     const int64_t m = a.t1 - a.m_base;
-    Kind kind = !direct_ok ? kLds
+    Kind kind = (splitg_ok && m <= 1024) ? kSplitG
+                : !direct_ok ? kLds
                 : (splitk_ok && m <= 1024) ? kSplitK
                 : (big_ok && m > 1024)     ? kBig
                 : (lds_fast_ok && m > 1024) ? kLds
@@ -1003,8 +1174,18 @@ Plan plan_for(const GemmArgs &a, bool tern, bool gs, bool single) {
         if (!strcmp(kv, "direct") && direct_ok) kind = kDirect;
         if (!strcmp(kv, "splitk") && splitk_ok) kind = kSplitK;
         if (!strcmp(kv, "big") && big_ok) kind = kBig;
+        if (!strcmp(kv, "splitg") && splitg_ok) kind = kSplitG;
     }
     if (kind == kBig) return Plan{kBig, 8, 4};
+    if (kind == kSplitG) {
+        static const Plan gtiles[] = {{kSplitG, 1, 8}, {kSplitG, 2, 4}, {kSplitG, 4, 2}};
+        const char *ge = getenv("VX_TILE");
+        int gm = 0, gn = 0;
+        if (ge && *ge && sscanf(ge, "%dx%d", &gm, &gn) == 2)
+            for (const Plan &t : gtiles)
+                if (gm == t.mt && gn == t.nt) return t;
+        return gtiles[0];
+    }
     static const Plan dtiles[] = {{kDirect, 4, 4}, {kDirect, 2, 4}, {kDirect, 2, 2}, {kDirect, 1, 2}, {kDirect, 1, 1}};
     static const Plan ltiles[] = {{kLds, 4, 4}, {kLds, 4, 2}, {kLds, 2, 4}};
     static const Plan stiles[] = {{kSplitK, 2, 4}, {kSplitK, 1, 8}, {kSplitK, 4, 2}};
@@ -1021,6 +1202,17 @@ Plan plan_for(const GemmArgs &a, bool tern, bool gs, bool single) {
     for (int i = 0; i < ntiles; i++)
         if (wgs_of(a, 16 * tiles[i].mt, 64 * tiles[i].nt) >= 1024) return tiles[i];
     return tiles[ntiles - 1];
+}
+
+template <int MT, int NT, bool TERN, bool GS>
+void launch_splitg(const GemmArgs &a, hipStream_t st) {
+    const dim3 grid((unsigned)((a.r1 - a.n_base + 16 * NT - 1) / (16 * NT)),
+                    (unsigned)((a.t1 - a.m_base + 16 * MT - 1) / (16 * MT)));
+    const int nsw = (int)(a.ng / 4) * 2;  // k-steps per wave (two per group)
+    if (nsw % 4 == 0)
+        tgemm_splitk_groups_kernel<MT, NT, TERN, GS, 2, 4><<<grid, 256, 0, st>>>(a);
+    else
+        tgemm_splitk_groups_kernel<MT, NT, TERN, GS, 2, 2><<<grid, 256, 0, st>>>(a);
 }
 
 template <int MT, int NT, bool TERN, bool GS>
@@ -1057,6 +1249,11 @@ void launch_splitk(const GemmArgs &a, hipStream_t st) {
                 FN<MT, NT, false, false>(__VA_ARGS__); \
         }                                              \
     } while (0)
+
+template <int MT, int NT>
+void run_splitg(const GemmArgs &a, bool tern, bool gs, hipStream_t st) {
+    VX_DISPATCH_TERN_GS(launch_splitg, a, st);
+}
 
 template <int MT, int NT>
 void run_splitk(const GemmArgs &a, bool tern, bool gs, hipStream_t st) {
@@ -1130,6 +1327,13 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
                      ? (a.bias ? tgemm_big_kernel<VX_EP_ADD_SCALED, true> : tgemm_big_kernel<VX_EP_ADD_SCALED, false>)
                      : (a.bias ? tgemm_big_kernel<VX_EP_STORE, true> : tgemm_big_kernel<VX_EP_STORE, false>);
         k<<<grid, 256, 0, st>>>(a);
+    } else if (p.kind == kSplitG) {
+        if (p.mt == 2 && p.nt == 4)
+            run_splitg<2, 4>(a, tern, g, st);
+        else if (p.mt == 1 && p.nt == 8)
+            run_splitg<1, 8>(a, tern, g, st);
+        else
+            run_splitg<4, 2>(a, tern, g, st);
     } else if (p.kind == kSplitK) {
         if (p.mt == 2 && p.nt == 4)
             run_splitk<2, 4>(a, tern, g, st);

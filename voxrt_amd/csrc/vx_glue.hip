@@ -53,63 +53,74 @@ void glu_dwconv_silu(const float *g, int64_t t, int64_t d, int64_t k, const floa
 
 // y[n][out] = x[n][in] . w[out][in]^T + b, each output with the reference tile's lane order: acc[l] =
 // fma(w[c + l], x[c + l], acc[l]) over 4-column steps, tail = sum of unfused w*x in order, y = (hsum4 + tail) + b,
-// optional ReLU. A 256-thread block computes 64 tokens x 64 outputs, a thread 4 x 4 of them, operands staged
-// through LDS in 32-column slabs.
-constexpr int LT = 64, LK = 32;
+// optional ReLU. The four running sums of one output are sequential by definition, so the parallelism is across
+// outputs. A 256-thread block owns 64 outputs x 16 tokens: lane l of every wavefront owns output o0 + l, wavefront
+// w tokens 4w .. 4w+3 (16 running sums per thread). Per 4-column step a lane reads its own weight quad from LDS
+// and the 4 token quads as LDS broadcasts, so LDS traffic stays below the FMA issue rate.
+constexpr int LO = 64, LTT = 16, LK = 64, LKP = LK + 4;
 
 template <bool RELU>
 __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict__ x, int n, int in_f,
                                                         const float *__restrict__ w, const float *__restrict__ b,
                                                         int out_f, float *__restrict__ y) {
-    __shared__ float xs[LT][LK + 1];
-    __shared__ float ws[LT][LK + 1];
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int t0 = blockIdx.y * LT, o0 = blockIdx.x * LT;
-    float acc[4][4][4];
+    __shared__ __attribute__((aligned(16))) float xs[LTT][LKP];
+    __shared__ __attribute__((aligned(16))) float ws[LO][LKP];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int t0 = blockIdx.y * LTT, o0 = blockIdx.x * LO;
+    float acc[4][4];
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-#pragma unroll
-            for (int l = 0; l < 4; l++) acc[a][c][l] = 0.0f;
+        for (int l = 0; l < 4; l++) acc[i][l] = 0.0f;
     const int c4 = in_f / 4 * 4;
+    const bool vec = (in_f % 4 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(w) % 16 == 0);
+    auto ld4 = [&](const float *base, int row, int nrows, int col) {
+        if (row >= nrows || col >= c4) return make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float *q = base + (int64_t)row * in_f + col;
+        return vec ? *(const float4 *)q : make_float4(q[0], q[1], q[2], q[3]);
+    };
+    // software pipeline: the next slab's quads are loaded into registers while the current slab is consumed
+    const int q = tid & 15, r = tid >> 4;
+    float4 pw[4], px;
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) pw[h] = ld4(w, o0 + r + 16 * h, out_f, k0 + q * 4);
+        px = ld4(x, t0 + r, n, k0 + q * 4);
+    };
+    if (c4 > 0) fetch(0);
     for (int k0 = 0; k0 < c4; k0 += LK) {
-        // stage x[t0 .. t0+63][k0 .. k0+31] and w[o0 .. o0+63][k0 .. k0+31] (zero outside; only columns < c4 are
-        // summed into the lanes, the tail is separate)
-        for (int e = threadIdx.x; e < LT * LK; e += 256) {
-            const int r = e / LK, kk = e % LK, col = k0 + kk;
-            const int tt = t0 + r, oo = o0 + r;
-            xs[r][kk] = (tt < n && col < c4) ? x[(int64_t)tt * in_f + col] : 0.0f;
-            ws[r][kk] = (oo < out_f && col < c4) ? w[(int64_t)oo * in_f + col] : 0.0f;
-        }
+#pragma unroll
+        for (int h = 0; h < 4; h++) *(float4 *)&ws[r + 16 * h][q * 4] = pw[h];
+        *(float4 *)&xs[r][q * 4] = px;
         __syncthreads();
+        if (k0 + LK < c4) fetch(k0 + LK);
         const int kend = min(LK, c4 - k0);
         for (int kk = 0; kk < kend; kk += 4) {
+            const float4 wa = *(const float4 *)&ws[lane][kk];
 #pragma unroll
-            for (int a = 0; a < 4; a++)
-#pragma unroll
-                for (int c = 0; c < 4; c++)
-#pragma unroll
-                    for (int l = 0; l < 4; l++)
-                        acc[a][c][l] = __builtin_fmaf(ws[tx * 4 + c][kk + l], xs[ty * 4 + a][kk + l], acc[a][c][l]);
+            for (int i = 0; i < 4; i++) {
+                const float4 xa = *(const float4 *)&xs[4 * wv + i][kk];
+                acc[i][0] = __builtin_fmaf(wa.x, xa.x, acc[i][0]);
+                acc[i][1] = __builtin_fmaf(wa.y, xa.y, acc[i][1]);
+                acc[i][2] = __builtin_fmaf(wa.z, xa.z, acc[i][2]);
+                acc[i][3] = __builtin_fmaf(wa.w, xa.w, acc[i][3]);
+            }
         }
         __syncthreads();
     }
+    const int o = o0 + lane;
+    if (o >= out_f) return;
 #pragma unroll
-    for (int a = 0; a < 4; a++) {
-        const int tt = t0 + ty * 4 + a;
-        if (tt >= n) continue;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int oo = o0 + tx * 4 + c;
-            if (oo >= out_f) continue;
-            float tail = 0.0f;
-            for (int col = c4; col < in_f; col++) tail += w[(int64_t)oo * in_f + col] * x[(int64_t)tt * in_f + col];
-            float v = ((acc[a][c][0] + acc[a][c][1]) + (acc[a][c][2] + acc[a][c][3])) + tail;
-            v = v + (b ? b[oo] : 0.0f);
-            if (RELU) v = v > 0.0f ? v : 0.0f;
-            y[(int64_t)tt * out_f + oo] = v;
-        }
+    for (int i = 0; i < 4; i++) {
+        const int t = t0 + 4 * wv + i;
+        if (t >= n) continue;
+        float tail = 0.0f;
+        for (int col = c4; col < in_f; col++) tail += w[(int64_t)o * in_f + col] * x[(int64_t)t * in_f + col];
+        float v = ((acc[i][0] + acc[i][1]) + (acc[i][2] + acc[i][3])) + tail;
+        v = v + (b ? b[o] : 0.0f);
+        if (RELU) v = v > 0.0f ? v : 0.0f;
+        y[(int64_t)t * out_f + o] = v;
     }
 }
 
@@ -159,8 +170,8 @@ void linear_f32(const float *x, int64_t n, int64_t in_f, const float *w, const f
         k<<<(unsigned)((out_f + 255) / 256), 256, 0, st>>>(x, (int)in_f, w, b, (int)out_f, y);
     } else {
         auto k = relu ? linear_f32_kernel<true> : linear_f32_kernel<false>;
-        k<<<dim3((unsigned)((out_f + LT - 1) / LT), (unsigned)((n + LT - 1) / LT)), 256, 0, st>>>(x, (int)n, (int)in_f,
-                                                                                                 w, b, (int)out_f, y);
+        k<<<dim3((unsigned)((out_f + LO - 1) / LO), (unsigned)((n + LTT - 1) / LTT)), 256, 0, st>>>(
+            x, (int)n, (int)in_f, w, b, (int)out_f, y);
     }
     hip_check(hipGetLastError(), "linear_f32 kernel launch");
 }
@@ -170,24 +181,44 @@ void linear_f32(const float *x, int64_t n, int64_t in_f, const float *w, const f
 __host__ __device__ inline int conv_out_len(int n, int k, int s, int p) { return (n + 2 * p - k) / s + 1; }
 
 // stage 0 (subsampling.rs:130-160): out[ot][of][ch] = relu(b[ch] + sum over (kt, kf) in order of w[kt*k+kf][ch] *
-// feats[ot*s + kt - p][of*s + kf - p]), out-of-range taps skipped.
+// feats[ot*s + kt - p][of*s + kf - p]), out-of-range taps skipped. A block is one output time row: the k input rows
+// it reads are staged in LDS (zero where out of range, never read there), each thread keeps one channel's taps.
+constexpr int kMaxMels = 256, kMaxK = 3;
 __global__ __launch_bounds__(256) void conv0_kernel(const float *__restrict__ feats, int t, int nm, int k, int s,
                                                    const float *__restrict__ w, const float *__restrict__ b, int c,
                                                    int t1, int f1, float *__restrict__ out) {
-    const int pos = blockIdx.x;  // ot * f1 + of
-    const int ot = pos / f1, of = pos % f1, p = (k - 1) / 2;
+    __shared__ float rows[kMaxK][kMaxMels];
+    const int ot = blockIdx.x, p = (k - 1) / 2;
+    for (int e = threadIdx.x; e < k * nm; e += blockDim.x) {
+        const int kt = e / nm, f = e % nm, it = ot * s + kt - p;
+        rows[kt][f] = (it >= 0 && it < t) ? feats[(int64_t)it * nm + f] : 0.0f;
+    }
+    __syncthreads();
     for (int ch = threadIdx.x; ch < c; ch += blockDim.x) {
-        float o = b[ch];
-        for (int kt = 0; kt < k; kt++) {
-            const int it = ot * s + kt - p;
-            if (it < 0 || it >= t) continue;
-            for (int kf = 0; kf < k; kf++) {
-                const int i_f = of * s + kf - p;
-                if (i_f < 0 || i_f >= nm) continue;
-                o = o + w[(kt * k + kf) * c + ch] * feats[(int64_t)it * nm + i_f];
-            }
+        float wk[kMaxK * kMaxK];
+#pragma unroll
+        for (int i = 0; i < kMaxK * kMaxK; i++) {
+            const int kt = i / kMaxK, kf = i % kMaxK;
+            wk[i] = (kt < k && kf < k) ? w[(kt * k + kf) * c + ch] : 0.0f;
         }
-        out[(int64_t)pos * c + ch] = o > 0.0f ? o : 0.0f;
+        const float bc = b[ch];
+        for (int of = 0; of < f1; of++) {
+            float o = bc;
+#pragma unroll
+            for (int kt = 0; kt < kMaxK; kt++) {
+                if (kt >= k) break;
+                const int it = ot * s + kt - p;
+                if (it < 0 || it >= t) continue;
+#pragma unroll
+                for (int kf = 0; kf < kMaxK; kf++) {
+                    if (kf >= k) break;
+                    const int i_f = of * s + kf - p;
+                    if (i_f < 0 || i_f >= nm) continue;
+                    o = o + wk[kt * kMaxK + kf] * rows[kt][i_f];
+                }
+            }
+            out[((int64_t)ot * f1 + of) * c + ch] = o > 0.0f ? o : 0.0f;
+        }
     }
 }
 
@@ -221,12 +252,13 @@ int64_t subsampling(const float *feats, int64_t t, int64_t nm, int64_t c, int64_
                     hipStream_t st) {
     require(feats && conv0_w && conv0_b && dw_w && dw_b && pw_w && pw_b && lin_w && lin_b && scratch && out,
             "subsampling: NULL pointer");
-    require(t > 0 && nm > 0 && c > 0 && k > 0 && s > 0 && c <= 1024, "subsampling: bad shape");
+    require(t > 0 && nm > 0 && nm <= kMaxMels && c > 0 && k > 0 && k <= kMaxK && s > 0 && c <= 1024,
+            "subsampling: bad shape (k <= 3, n_mels <= 256)");
     const int p = (int)(k - 1) / 2;
     const int t1 = conv_out_len((int)t, (int)k, (int)s, p), f1 = conv_out_len((int)nm, (int)k, (int)s, p);
     require((int64_t)t1 * f1 * c < (1ll << 31), "subsampling: input too long");
     float *a = scratch, *bbuf = scratch + (int64_t)t1 * f1 * c;
-    conv0_kernel<<<(unsigned)(t1 * f1), 256, 0, st>>>(feats, (int)t, (int)nm, (int)k, (int)s, conv0_w,
+    conv0_kernel<<<(unsigned)t1, 256, 0, st>>>(feats, (int)t, (int)nm, (int)k, (int)s, conv0_w,
                                                                 conv0_b, (int)c, t1, f1, a);
     hip_check(hipGetLastError(), "conv0 kernel launch");
     int tc = t1, fc = f1;

@@ -147,6 +147,200 @@ __global__ __launch_bounds__(256) void quantize_fast_kernel(const float *__restr
     }
 }
 
+// Row-resident path: inp = NC * 1024 (NC <= 4), one wavefront per token, the row loaded once into registers
+// (16 consecutive floats per lane per 1024-column chunk). With LN the row is also staged in the wavefront's LDS
+// slot, where lanes 0-7 run the reference-order statistics. MODE 0 quantizes, MODE 1 writes the LayerNorm row as
+// float32 (y). Waves of pad tokens [n, np) only write zero scales and code sums, so no pad launch is needed.
+template <int L, int NC, bool LN, int MODE>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict__ x, int n, int np, int group,
+                                                        int8_t *__restrict__ q, float *__restrict__ st,
+                                                        int32_t *__restrict__ gt, const float *__restrict__ lg,
+                                                        const float *__restrict__ lb, float *__restrict__ y) {
+    constexpr int inp = NC * 1024;
+    __shared__ __attribute__((aligned(16))) float srow[LN ? 4 : 1][LN ? inp : 4];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + w;
+    if (t >= np) return;
+    const int ng = inp / group;
+    if (t >= n) {
+        if (MODE == 0)
+            for (int g = lane; g < ng; g += 64) {
+                st[(int64_t)g * np + t] = 0.0f;
+                gt[(int64_t)g * np + t] = 0;
+            }
+        return;
+    }
+    const float *xr = x + (int64_t)t * inp;
+    float4 lgv[LN ? NC : 1][4], lbv[LN ? NC : 1][4];  // gamma / beta quads, fetched with the row
+    if constexpr (LN) {
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lgv[c][i] = ((const float4 *)(lg + c * 1024 + lane * 16))[i];
+                lbv[c][i] = ((const float4 *)(lb + c * 1024 + lane * 16))[i];
+            }
+    }
+    float v[NC][16];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const float4 *p = (const float4 *)(xr + c * 1024 + lane * 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 f = p[i];
+            v[c][4 * i] = f.x;
+            v[c][4 * i + 1] = f.y;
+            v[c][4 * i + 2] = f.z;
+            v[c][4 * i + 3] = f.w;
+        }
+    }
+    if constexpr (LN) {
+        // the row transposed by column residue: T[j][k] = x[8k + j], so that the running sum of residue j (the
+        // reference's lane j of row_mean_var_portable) walks contiguous memory
+        constexpr int KL = inp / 8;
+        float *T = srow[w];
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                *(float2 *)(T + j * KL + c * 128 + 2 * lane) = make_float2(v[c][j], v[c][8 + j]);
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's row is in LDS
+        __builtin_amdgcn_wave_barrier();
+        float mean, linv;
+        // lane j < 8 keeps the running sum of columns j, j+8, j+16, ... in that order
+        float s = 0.0f;
+        if (lane < 8) {
+            const float *r = T + lane * KL;
+#pragma unroll 4
+            for (int k = 0; k < KL; k += 4) {
+                const float4 f = *(const float4 *)(r + k);
+                s += f.x;
+                s += f.y;
+                s += f.z;
+                s += f.w;
+            }
+        }
+        float pr = s + __shfl(s, lane + 4, 64);
+        float sum = (pr + __shfl(pr, 1, 64)) + (__shfl(pr, 2, 64) + __shfl(pr, 3, 64));
+        sum = __shfl(sum, 0, 64);
+        mean = sum / (float)inp;
+        float qs = 0.0f;
+        if (lane < 8) {
+            const float *r = T + lane * KL;
+#pragma unroll 4
+            for (int k = 0; k < KL; k += 4) {
+                const float4 f = *(const float4 *)(r + k);
+                float a = f.x - mean;
+                qs = __builtin_fmaf(a, a, qs);
+                a = f.y - mean;
+                qs = __builtin_fmaf(a, a, qs);
+                a = f.z - mean;
+                qs = __builtin_fmaf(a, a, qs);
+                a = f.w - mean;
+                qs = __builtin_fmaf(a, a, qs);
+            }
+        }
+        pr = qs + __shfl(qs, lane + 4, 64);
+        float sq = (pr + __shfl(pr, 1, 64)) + (__shfl(pr, 2, 64) + __shfl(pr, 3, 64));
+        sq = __shfl(sq, 0, 64);
+        const float var = sq / (float)inp;
+        linv = 1.0f / __builtin_sqrtf(var + 1e-5f);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 g4 = lgv[c][i], b4 = lbv[c][i];
+                v[c][4 * i] = ln_apply(v[c][4 * i], mean, linv, g4.x, b4.x);
+                v[c][4 * i + 1] = ln_apply(v[c][4 * i + 1], mean, linv, g4.y, b4.y);
+                v[c][4 * i + 2] = ln_apply(v[c][4 * i + 2], mean, linv, g4.z, b4.z);
+                v[c][4 * i + 3] = ln_apply(v[c][4 * i + 3], mean, linv, g4.w, b4.w);
+            }
+        }
+    }
+    if constexpr (MODE == 1) {
+        float *yr = y + (int64_t)t * inp;
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                *(float4 *)(yr + c * 1024 + lane * 16 + 4 * i) =
+                    make_float4(v[c][4 * i], v[c][4 * i + 1], v[c][4 * i + 2], v[c][4 * i + 3]);
+        return;
+    }
+    // groups of L lanes (group = 16 L columns) or whole chunks (L = 64, group = 1024 * k)
+    int8_t *qr = q + (int64_t)t * inp;
+    constexpr int CPG = 1;  // chunks per group when L == 64 is handled below
+    (void)CPG;
+    if (L < 64 || group == 1024) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            float m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[c][i]));
+#pragma unroll
+            for (int o = 1; o < L; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            const float sc = m == 0.0f ? 1.0f : m / 127.0f;
+            const float inv = 1.0f / sc;
+            int sum = 0;
+            uint32_t wd[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int8_t c0 = code_of(v[c][4 * i], inv), c1 = code_of(v[c][4 * i + 1], inv),
+                             c2 = code_of(v[c][4 * i + 2], inv), c3 = code_of(v[c][4 * i + 3], inv);
+                sum += (int)c0 + (int)c1 + (int)c2 + (int)c3;
+                wd[i] = (uint32_t)(uint8_t)c0 | ((uint32_t)(uint8_t)c1 << 8) | ((uint32_t)(uint8_t)c2 << 16) |
+                        ((uint32_t)(uint8_t)c3 << 24);
+            }
+            *(uint4 *)(qr + c * 1024 + lane * 16) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+#pragma unroll
+            for (int o = 1; o < L; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            if ((lane & (L - 1)) == 0) {
+                const int g = (c * 1024 + lane * 16) / group;
+                st[(int64_t)g * np + t] = sc;
+                gt[(int64_t)g * np + t] = sum;
+            }
+        }
+    } else {
+        // one group spans several chunks (group = 1024 * k): reduce over the chunks of each group
+        const int cpg = group / 1024;
+        for (int c0 = 0; c0 < NC; c0 += cpg) {
+            float m = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+                if (c >= c0 && c < c0 + cpg)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[c][i]));
+            m = fmaxf(m, 0.0f);
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            const float sc = m == 0.0f ? 1.0f : m / 127.0f;
+            const float inv = 1.0f / sc;
+            int sum = 0;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                if (c < c0 || c >= c0 + cpg) continue;
+                uint32_t wd[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int8_t a0 = code_of(v[c][4 * i], inv), a1 = code_of(v[c][4 * i + 1], inv),
+                                 a2 = code_of(v[c][4 * i + 2], inv), a3 = code_of(v[c][4 * i + 3], inv);
+                    sum += (int)a0 + (int)a1 + (int)a2 + (int)a3;
+                    wd[i] = (uint32_t)(uint8_t)a0 | ((uint32_t)(uint8_t)a1 << 8) | ((uint32_t)(uint8_t)a2 << 16) |
+                            ((uint32_t)(uint8_t)a3 << 24);
+                }
+                *(uint4 *)(qr + c * 1024 + lane * 16) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+            }
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            if (lane == 0) {
+                const int g = c0 / cpg;
+                st[(int64_t)g * np + t] = sc;
+                gt[(int64_t)g * np + t] = sum;
+            }
+        }
+    }
+}
+
 // Any group that divides inp: one group at a time across the wavefront.
 template <bool LN>
 __global__ __launch_bounds__(256) void quantize_generic_kernel(const float *__restrict__ x, int n, int inp,
@@ -216,6 +410,31 @@ void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const fl
         else if (group >= 64 && group <= 1024 && (group & (group - 1)) == 0)
             L = group / 16;
     }
+    const int nc = (int)(inp / 1024);
+    if (L != 0 && inp <= 4096) {  // the row-resident kernel covers the pad tokens too
+        const unsigned blk = (unsigned)((np + 3) / 4);
+#define VX_QR(LL, NC)                                                                                                \
+    (ln ? quant_rows_kernel<LL, NC, true, 0> : quant_rows_kernel<LL, NC, false, 0>)<<<blk, 256, 0, stream>>>(       \
+        x, ni, np, gi, q, scales_t, gsum_t, g, b, nullptr)
+#define VX_QR_NC(LL)                                                                                                 \
+    switch (nc) {                                                                                                    \
+        case 1: VX_QR(LL, 1); break;                                                                                 \
+        case 2: VX_QR(LL, 2); break;                                                                                 \
+        case 3: VX_QR(LL, 3); break;                                                                                 \
+        default: VX_QR(LL, 4); break;                                                                                \
+    }
+        switch (L) {
+            case 4: VX_QR_NC(4); break;
+            case 8: VX_QR_NC(8); break;
+            case 16: VX_QR_NC(16); break;
+            case 32: VX_QR_NC(32); break;
+            default: VX_QR_NC(64); break;
+        }
+#undef VX_QR_NC
+#undef VX_QR
+        hip_check(hipGetLastError(), "quantize kernel launch");
+        return;
+    }
 #define VX_QF(LL)                                                                                                    \
     (ln ? quantize_fast_kernel<LL, true> : quantize_fast_kernel<LL, false>)<<<blocks, 256, 0, stream>>>(           \
         x, ni, ii, gi, np, q, scales_t, gsum_t, g, b)
@@ -262,6 +481,19 @@ void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const floa
     require(x && g && b && y, "x, gamma, beta and y must not be NULL");
     require(n >= 0 && d > 0 && n * d < (1ll << 31), "bad LayerNorm shape");
     if (n == 0) return;
+    auto al16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (d % 1024 == 0 && d <= 4096 && al16(x) && al16(y) && al16(g) && al16(b)) {
+        const unsigned blk = (unsigned)((n + 3) / 4);
+        const int ni = (int)n;
+        switch (d / 1024) {
+            case 1: quant_rows_kernel<4, 1, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y); break;
+            case 2: quant_rows_kernel<4, 2, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y); break;
+            case 3: quant_rows_kernel<4, 3, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y); break;
+            default: quant_rows_kernel<4, 4, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y); break;
+        }
+        hip_check(hipGetLastError(), "layer_norm kernel launch");
+        return;
+    }
     layer_norm_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(x, (int)n, (int)d, g, b, y);
     hip_check(hipGetLastError(), "layer_norm kernel launch");
 }
