@@ -110,6 +110,21 @@ def time_launches(torch, gemms, reps, replays=5):
     return out
 
 
+def traffic_of(g):
+    """HBM bytes per launch of the dominant GEMM, from the committed rocprofv3 --pmc summary
+    (profiles/tgemm_traffic.json: FETCH_SIZE and WRITE_SIZE of this GEMM's kernel in the default bench run, each
+    scaled by the same counter's reading for a plain copy of known size); None when absent or for another shape."""
+    path = os.path.join(ROOT, "profiles", "tgemm_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("shape") != f"{g.m}x{g.k}x{g.n}:G{g.group}":
+        return None
+    return t.get("traffic_bytes")
+
+
 def roofline_of(g, sec):
     t_mfma = g.ops / (PEAK_INT8_TOPS * 1e12)
     t_hbm = g.bytes / (PEAK_HBM_GBS * 1e9)
@@ -249,6 +264,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-details", action="store_true")
     ap.add_argument("--no-encoder", action="store_true", help="skip the 24-layer encoder RTFx leg")
+    ap.add_argument("--encoder-only", action="store_true",
+                    help="only the 24-layer encoder RTFx leg (prints its JSON and exits)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run a plain 256 MiB device copy 5 times (the counter calibration of the traffic figure)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the ternary GEMM path shards by "
@@ -258,11 +277,28 @@ def main():
 
     import torch
 
+    if args.copy_calib:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes": src.numel() * 4, "dispatches": 5}), flush=True)
+        return
+
     import voxrt_amd as vx
     from voxrt_amd import synth
 
     vx.kernels.check(vx.lib().vx_init(0))
     dev = torch.device("cuda:0")
+    if args.encoder_only:
+        enc, eparams, esp = encoder_setup(synth)
+        out = {"encoder": encoder_rtfx(torch, synth, enc, dev)}
+        enc.free()
+        if not args.no_cpu:
+            out["encoder_cpu"] = cpu_encoder_rtfx(eparams, esp, synth)
+        print(json.dumps(out), flush=True)
+        return
     T = 338
     gemms = [Gemm(vx, synth, dev, name, m, k, n, ep, a, k, 1, 16 * i + 1)
              for i, (name, m, k, n, ep, a) in enumerate(layer_shapes(T))]
@@ -291,8 +327,8 @@ def main():
     per = time_launches(torch, gemms, 20)
     dom = max(gemms, key=lambda g: per[g.name])
     roof = roofline_of(dom, per[dom.name])
-    roof["kernel"] = f"tgemm_kernel ({dom.name}: M={dom.m} K={dom.k} N={dom.n} G={dom.group})"
-    roof["traffic"] = None
+    roof["kernel"] = f"ternary GEMM {dom.name}: M={dom.m} K={dom.k} N={dom.n} G={dom.group} (split-K kernel)"
+    roof["traffic"] = traffic_of(dom)
 
     details = {"per_gemm_us": {g.name: round(per[g.name] * 1e6, 2) for g in gemms}}
     if not args.no_details:
