@@ -383,3 +383,42 @@ def test_large_token_kernel_ranges_with_nan_canary(dev, orc):
         inside[t0:t1, r0:r1] = True
         assert (np.isnan(got) == ~inside).all(), f"stray write rows {r0}..{r1} toks {t0}..{t1}"
         _assert_bits_equal(got[inside], want[inside], f"rows {r0}..{r1} toks {t0}..{t1}")
+
+
+@pytest.mark.parametrize("m,k,n_out,grid", [(1536, 1024, 2048, 16), (1536 + 37, 1024, 1024, 8),
+                                            (1024, 4096, 1024, 8), (2048, 1024, 3072, 0)])
+def test_stream_kernel_every_output(dev, orc, m, k, n_out, grid):
+    """The streaming large-token kernel (whole 128 x 256 tiles, G = K), forced on shapes the oracle checks in
+    full: several tiles per workgroup (a small grid), so each tile's epilogue runs while the next tile computes;
+    K = 4096 (the general step loop); a ragged token count whose last 37 rows go through another kernel; each
+    epilogue with and without bias, every output bit-exact."""
+    import torch
+
+    import voxrt_amd as vx
+
+    trits, s16, x = _workload(orc, m, k, n_out, k, seed_cfg=5)
+    ws = orc.f16_to_f32(s16)
+    w = vx.TernaryMatrix.from_packed_f32(synth.pack_rows(trits), ws, n_out, k, k)
+    q, xs, _ = orc.quantize(x, k)
+    xa = vx.QuantAct.quantize(_t(x, dev), k)
+    rng = synth.Lcg(41)
+    base = ((rng.take(m * n_out) % 200).astype(np.float32) * np.float32(0.01) - np.float32(1.0)).reshape(m, n_out)
+    bias = (rng.take(n_out) % 100).astype(np.float32) / np.float32(10.0)
+    old = {v: os.environ.get(v) for v in ("VX_GEMM", "VX_STREAM_GRID")}
+    os.environ["VX_GEMM"] = "stream"
+    os.environ["VX_STREAM_GRID"] = str(grid)
+    try:
+        for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
+            want = orc.gemm(trits, ws, q, xs, k, y=base.copy(), ep=ep_kind, alpha=alpha)
+            for with_bias in (False, True):
+                y = _t(base, dev)
+                vx.gemm_ep(w, xa, y, _t(bias, dev) if with_bias else None, _ep_of(vx, ep_kind, alpha))
+                exp = (want + bias[None, :]).astype(np.float32) if with_bias else want
+                _assert_bits_equal(y.cpu().numpy(), exp, f"stream {m}x{k}x{n_out} grid={grid} ep={ep_kind} "
+                                                         f"bias={with_bias}")
+    finally:
+        for v, val in old.items():
+            if val is None:
+                os.environ.pop(v, None)
+            else:
+                os.environ[v] = val

@@ -28,35 +28,9 @@
 // guarded by the [t0, t1) x [r0, r1) window.
 #include <cstring>
 
-#include "vx_internal.h"
+#include "vx_gemm.h"
 
 namespace vx {
-
-struct GemmArgs {
-    const void *w;          // ternary: uint32 codes; int8: 16-byte chunks (see TMat)
-    const float *ws_t;      // [ng][out_pad]
-    const int8_t *xq;       // [n][inp]
-    const float *xs;        // scales_t [ng][np]
-    const int32_t *xg;      // gsum_t [ng][np] (ternary only)
-    float *y;               // [n][out]
-    const float *bias;      // [out] or NULL
-    int32_t *gs;            // [ng][n][out] or NULL
-    int64_t n, np, out, inp, ng, out_pad, spg;
-    int64_t r0, r1, t0, t1, n_base, m_base;
-    uint32_t w_bytes, ws_bytes, xq_bytes, xs_bytes, y_bytes;
-    int ep;
-    float alpha;
-    int vec_ok;  // y (and bias) rows are 16-byte aligned: out % 4 == 0 and 16-byte aligned base pointers
-};
-
-__device__ inline v4i widen_codes(uint32_t p) {
-    v4i r;
-    r.x = (int)(p & 0x03030303u);
-    r.y = (int)((p >> 2) & 0x03030303u);
-    r.z = (int)((p >> 4) & 0x03030303u);
-    r.w = (int)((p >> 6) & 0x03030303u);
-    return r;
-}
 
 // int32 group sums of group g to gs[(g*n + t)*out + o] inside the [t0, t1) x [r0, r1) window
 template <int MT, int NT>
@@ -1317,6 +1291,16 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
     a.ep = ep;
     a.alpha = alpha;
     const bool tern = w->ternary, g = gs != nullptr, single = w->ng == 1;
+    // whole 128-token tiles of a full-width single-group ternary GEMM: the streaming kernel; the remaining tokens
+    // (fewer than 128) go through the kernels below
+    if (tern && single && !g && r0 == 0 && r1 == w->out && t0 == 0 && n >= 128) {
+        const int64_t full = n / 128 * 128;
+        if (full < (1ll << 30) && gemm_stream(a, (int)full, st)) {
+            if (full == n) return;
+            a.t0 = full;
+            a.m_base = full;
+        }
+    }
     a.vec_ok = (w->out % 4 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
                (!bias || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
     const Plan p = plan_for(a, tern, g, single);
