@@ -194,26 +194,90 @@ def encoder_setup(synth, n_layers=24):
 
 def encoder_rtfx(torch, synth, enc, dev, reps=5):
     """Device time of encoder forwards from log-mel features (subsampling + 24 layers, each frame count replayed
-    from its hipGraph), as RTFx = audio seconds / encoder seconds."""
+    from its hipGraph), as RTFx = audio seconds / encoder seconds. Several segments of one length go through one
+    batched forward (each segment's output equals its own forward); "sequential_ms" times the same segments one
+    forward at a time."""
     out = {}
     for name, t_in, nseg in ENC_WORKLOADS:
-        feats = torch.from_numpy(synth.synth_normal(synth.workload_seed(4, t_in & 0xFF), t_in * 128)
-                                 .reshape(t_in, 128)).to(dev)
-        y = enc.forward_feats(feats)  # first call: workspace, graph capture
-        enc.forward_feats(feats, out=y)
+        feats = torch.from_numpy(synth.synth_normal(synth.workload_seed(4, t_in & 0xFF), nseg * t_in * 128)
+                                 .reshape(nseg, t_in, 128)).to(dev)
+
+        def run(y):
+            if nseg == 1:
+                enc.forward_feats(feats[0], out=y[0])
+            else:
+                enc.forward_feats_batch(feats, out=y)
+
+        y = torch.empty((nseg, enc.out_frames(t_in), enc.d), dtype=torch.float32, device=dev)
+        run(y)  # first call: workspace, graph capture
+        run(y)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(reps):
-            for _ in range(nseg):
-                enc.forward_feats(feats, out=y)
+            run(y)
         e1.record()
         torch.cuda.synchronize()
         sec = e0.elapsed_time(e1) * 1e-3 / reps
         audio = t_in * nseg / 100.0
         out[name] = {"frames": enc.out_frames(t_in), "segments": nseg, "audio_s": audio, "ms": round(sec * 1e3, 3),
                      "rtfx": round(audio / sec, 1)}
+        if nseg > 1:
+            y1 = enc.forward_feats(feats[0])
+            torch.cuda.synchronize()
+            e0.record()
+            for s in range(nseg):
+                enc.forward_feats(feats[s], out=y1)
+            e1.record()
+            torch.cuda.synchronize()
+            out[name]["sequential_ms"] = round(e0.elapsed_time(e1), 3)
+            del y1
+        del y
     return out
+
+
+def clip_batch_tops(torch, vx, synth, dev, params, reps=3):
+    """64 short clips (25 + lcg % 164 frames each, 2-15 s) concatenated to M rows of per-token int8 activations
+    (group = K) through the linear layers of all 24 layers (ff1 up/down, q|k|v, out, pw1, pw2, ff2 up/down; the
+    position projection depends on each clip's length and is left out), per-output-channel scales. Returns the
+    aggregate TOPS of one pass over the 192 GEMMs."""
+    lens = 25 + synth.Lcg(synth.workload_seed(2, 0)).take(64) % 164
+    m = int(lens.sum())
+    names = ("ff1_w1", "ff1_w2", "qkv", "o", "pw1", "pw2", "ff2_w1", "ff2_w2")
+    acts = {}
+    for k in (1024, 4096):
+        x = torch.from_numpy(synth.synth_normal(synth.workload_seed(2, k >> 10), m * k).reshape(m, k)).to(dev)
+        acts[k] = vx.QuantAct.quantize(x, k)
+        del x
+    work, ops, ys = [], 0.0, {}
+    for p in params:
+        for n in names:
+            q, s16 = p["linears"][n]
+            out, inp = s16.shape[0], s16.shape[1] * 128
+            w = vx.TernaryMatrix.from_packed(q, np.ascontiguousarray(s16[:, :1]), out, inp, inp)
+            if out not in ys:  # one output buffer per width: the GEMMs run one after another
+                ys[out] = torch.empty((m, out), dtype=torch.float32, device=dev)
+            work.append((w, acts[inp], ys[out]))
+            ops += 2.0 * m * out * inp
+
+    def step():
+        for w, a, y in work:
+            vx.gemm_ep(w, a, y, None, vx.Epilogue.Store)
+
+    graph = capture(torch, step)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / reps
+    del graph, work, acts, ys
+    torch.cuda.empty_cache()
+    return {"clips": 64, "rows": m, "gemms": 192, "ms": round(sec * 1e3, 3), "tops": round(ops / sec / 1e12, 1),
+            "pct_int8_peak": round(100 * ops / sec / 1e12 / PEAK_INT8_TOPS, 1)}
 
 
 def cpu_encoder_rtfx(params, sp, synth, budget_s=30.0):
@@ -351,6 +415,8 @@ def main():
         enc, eparams, esp = encoder_setup(synth)
         details["encoder"] = encoder_rtfx(torch, synth, enc, dev)
         enc.free()
+        if not args.no_details:
+            details["clip_batch_24_layers"] = clip_batch_tops(torch, vx, synth, dev, eparams)
         if not args.no_cpu:
             ce = cpu_encoder_rtfx(eparams, esp, synth)
             details["encoder_cpu"] = ce

@@ -201,6 +201,15 @@ vx_status vx_encoder_forward(vx_encoder *enc, const float *x, float *out, int64_
  * for vx_subsampling_frames(t_in, sub_kernel, sub_stride) rows). */
 vx_status vx_encoder_forward_feats(vx_encoder *enc, const float *feats, int64_t t_in, float *out, int64_t *t_out,
                                    void *stream);
+/* Batched forms: nseg segments of equal length in one pass, x / feats / out laid out [nseg][t][...]. Each segment's
+ * output equals its own vx_encoder_forward(_feats) bit for bit: token-row work (LayerNorm, quantizers, GEMMs)
+ * runs over all nseg * t rows at once, while the depthwise convolution, the attention and the subsampling stay
+ * inside each segment. The reference encodes one VAD segment per call (Transcriber::transcribe_long,
+ * transcriber.rs:356-386); these entry points have no counterpart there and serve callers that hold several
+ * segments of one length at once. nseg * t <= 65535; a workspace is kept per distinct (t, nseg). */
+vx_status vx_encoder_forward_batch(vx_encoder *enc, const float *x, float *out, int64_t nseg, int64_t t, void *stream);
+vx_status vx_encoder_forward_feats_batch(vx_encoder *enc, const float *feats, int64_t nseg, int64_t t_in, float *out,
+                                         int64_t *t_out, void *stream);
 void vx_encoder_free(vx_encoder *enc);
 
 #ifdef __cplusplus

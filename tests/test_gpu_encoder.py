@@ -221,3 +221,73 @@ def test_encoder_feats_equal_oracle(dev, orc):
     assert got.shape == (t, 1024) == (enc.out_frames(t_in), 1024)
     _bits_equal(got, want, "encoder from features")
     enc.free()
+
+
+def test_encoder_batch_equals_oracle(dev, orc):
+    """Three segments of t=29 frames in one batched pass through two full-width layers (graphs on, two replays):
+    every segment equals the CPU int8 layer restatement of that segment alone, bit for bit (the batched GEMMs see
+    87 rows, the attention and the depthwise convolution stay inside each segment)."""
+    from voxrt_amd import encoder as E
+
+    nseg, t, L = 3, 29, 2
+    params = [synth.synth_layer(10 + i) for i in range(L)]
+    enc = E.Encoder(n_layers=L)
+    for i, p in enumerate(params):
+        enc.set_layer(i, p)
+    x = _x(31, nseg, t, 1024)
+    pos = orc.rel_pos_table(t, 1024)
+    want = []
+    for s in range(nseg):
+        y = x[s].copy()
+        for p in params:
+            y = orc.conformer_layer(y, pos, _oracle_layer(orc, p), heads=8)
+        want.append(y)
+    xd = _t(x, dev)
+    for rep in range(2):
+        got = enc.forward_batch(xd).cpu().numpy()
+        assert got.shape == (nseg, t, 1024)
+        for s in range(nseg):
+            _bits_equal(got[s], want[s], f"batched encoder segment {s} (pass {rep})")
+    enc.free()
+
+
+def test_encoder_feats_batch_equals_oracle(dev, orc):
+    """Four segments of 120 log-mel frames (15 frames after subsampling) through subsampling and one layer in one
+    batched pass: each segment equals the oracle's subsampling + layer of that segment, bit for bit."""
+    from voxrt_amd import encoder as E
+
+    nseg, t_in = 4, 120
+    p = synth.synth_layer(6)
+    sp = synth.synth_subsampling()
+    enc = E.Encoder(n_layers=1)
+    enc.set_layer(0, p)
+    enc.set_subsampling(sp)
+    feats = _x(32, nseg, t_in, 128)
+    got = enc.forward_feats_batch(_t(feats, dev)).cpu().numpy()
+    lp = _oracle_layer(orc, p)
+    for s in range(nseg):
+        x = orc.subsampling(feats[s], sp)
+        t = x.shape[0]
+        want = orc.conformer_layer(x, orc.rel_pos_table(t, 1024), lp, heads=8)
+        assert got.shape == (nseg, t, 1024)
+        _bits_equal(got[s], want, f"batched features segment {s}")
+    enc.free()
+
+
+def test_encoder_batch_of_32_equals_single_segments(dev):
+    """32 segments of 125 frames (the 32 x 10 s workload: 4000 rows, so the GEMMs take the large-token kernels)
+    through one layer: each segment of the batched pass equals the single-segment pass of that segment."""
+    import torch
+
+    from voxrt_amd import encoder as E
+
+    nseg, t = 32, 125
+    enc = E.Encoder(n_layers=1)
+    enc.set_layer(0, synth.synth_layer(7))
+    x = _t(_x(33, nseg, t, 1024), dev)
+    got = enc.forward_batch(x).cpu().numpy()
+    for s in (0, 1, 17, 31):
+        one = enc.forward(x[s].contiguous()).cpu().numpy()
+        _bits_equal(got[s], one, f"batch of 32, segment {s}")
+    torch.cuda.synchronize()
+    enc.free()

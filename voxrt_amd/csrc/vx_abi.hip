@@ -42,6 +42,9 @@ void encoder_use_graphs(vx_encoder *e, bool on);
 void encoder_set_layer(vx_encoder *e, int64_t li, const vx_layer_params *p);
 void encoder_set_subsampling(vx_encoder *e, const vx_subsampling_params *p);
 void encoder_forward(vx_encoder *e, const float *x, float *out, int64_t t, hipStream_t st);
+void encoder_forward_batch(vx_encoder *e, const float *x, float *out, int64_t nseg, int64_t t, hipStream_t st);
+void encoder_forward_feats_batch(vx_encoder *e, const float *feats, int64_t nseg, int64_t t_in, float *out,
+                                 int64_t *t_out, hipStream_t st);
 void encoder_forward_feats(vx_encoder *e, const float *feats, int64_t t_in, float *out, int64_t *t_out,
                            hipStream_t st);
 }  // namespace vx
@@ -278,6 +281,15 @@ vx_status vx_encoder_forward(vx_encoder *enc, const float *x, float *out, int64_
 vx_status vx_encoder_forward_feats(vx_encoder *enc, const float *feats, int64_t t_in, float *out, int64_t *t_out,
                                    void *stream) {
     return guarded([&] { vx::encoder_forward_feats(enc, feats, t_in, out, t_out, (hipStream_t)stream); });
+}
+
+vx_status vx_encoder_forward_batch(vx_encoder *enc, const float *x, float *out, int64_t nseg, int64_t t, void *stream) {
+    return guarded([&] { vx::encoder_forward_batch(enc, x, out, nseg, t, (hipStream_t)stream); });
+}
+
+vx_status vx_encoder_forward_feats_batch(vx_encoder *enc, const float *feats, int64_t nseg, int64_t t_in, float *out,
+                                         int64_t *t_out, void *stream) {
+    return guarded([&] { vx::encoder_forward_feats_batch(enc, feats, nseg, t_in, out, t_out, (hipStream_t)stream); });
 }
 
 void vx_encoder_free(vx_encoder *enc) { vx::encoder_free(enc); }

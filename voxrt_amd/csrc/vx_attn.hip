@@ -35,6 +35,7 @@ __host__ __device__ inline int up64(int x) { return (x + 63) / 64 * 64; }
 
 struct AttnDims {
     int t, d, h, np, tp, rp, tv;
+    int nseg = 1;  // segments of t frames each: qkv and ctx are [nseg][t][...], the relative rows are shared
     __host__ __device__ AttnDims(int t_, int d_, int h_) : t(t_), d(d_), h(h_) {
         np = 2 * t - 1;
         tp = up16(t);       // token rows (queries, keys)
@@ -67,16 +68,19 @@ __device__ inline float quant128(float a0, float a1, int lane, int8_t *dst) {
     return s;
 }
 
-// Work items: [0, h*tp) query/key rows (head-major), then [h*tp, h*(tp+rp)) relative rows.
+// Work items: [0, nseg*h*tp) query/key rows (segment-major, then head-major), then h*rp relative rows (shared).
 __global__ __launch_bounds__(256) void attn_rows_kernel(const float *__restrict__ qkv, const float *__restrict__ rel_k,
                                                        const float *__restrict__ bias_u,
                                                        const float *__restrict__ bias_v, AttnDims D, AttnWs W) {
     const int lane = threadIdx.x & 63;
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int d3 = 3 * D.d;
-    if (item < D.h * D.tp) {
-        const int h = item / D.tp, i = item % D.tp;
-        const int64_t o = ((int64_t)h * D.tp + i) * kDh;
+    if (item < D.nseg * D.h * D.tp) {
+        const int seg = item / (D.h * D.tp), hi = item % (D.h * D.tp);
+        const int h = hi / D.tp, i = hi % D.tp;
+        qkv += (int64_t)seg * D.t * d3;
+        const int64_t so = (int64_t)seg * D.h * D.tp;  // this segment's rows of the per-token tables
+        const int64_t o = (so + (int64_t)h * D.tp + i) * kDh;
         float q0 = 0.0f, q1 = 0.0f, k0 = 0.0f, k1 = 0.0f;
         if (i < D.t) {
             const float2 qq = *(const float2 *)(qkv + (int64_t)i * d3 + h * kDh + 2 * lane);
@@ -93,13 +97,13 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(const float *__restrict_
         const float sv = quant128(live ? q0 + bv.x : 0.0f, live ? q1 + bv.y : 0.0f, lane, W.qv + o);
         const float sk = quant128(k0, k1, lane, W.kq + o);
         if (lane == 0) {
-            W.qus[h * D.tp + i] = su;
-            W.qvs[h * D.tp + i] = sv;
-            W.ks[h * D.tp + i] = sk;
+            W.qus[so + h * D.tp + i] = su;
+            W.qvs[so + h * D.tp + i] = sv;
+            W.ks[so + h * D.tp + i] = sk;
         }
         return;
     }
-    const int r = item - D.h * D.tp;
+    const int r = item - D.nseg * D.h * D.tp;
     if (r >= D.h * D.rp) return;
     const int h = r / D.rp, p = r % D.rp;
     float a0 = 0.0f, a1 = 0.0f;
@@ -112,22 +116,23 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(const float *__restrict_
     if (lane == 0) W.rs[h * D.rp + p] = s;
 }
 
-// One wavefront per (head, channel): vT row = v[i][h*dh + c] for i < t, zero to tv; one group.
+// One wavefront per (segment, head, channel): vT row = v[i][h*dh + c] for i < t, zero to tv; one group.
 __global__ __launch_bounds__(256) void attn_vt_kernel(const float *__restrict__ qkv, AttnDims D, AttnWs W) {
     const int lane = threadIdx.x & 63;
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= D.h * kDh) return;
-    const int h = item / kDh, c = item % kDh;
-    const float *col = qkv + 2 * D.d + h * kDh + c;
+    if (item >= D.nseg * D.h * kDh) return;
+    const int seg = item / (D.h * kDh), hc = item % (D.h * kDh);
+    const int h = hc / kDh, c = hc % kDh;
+    const float *col = qkv + (int64_t)seg * D.t * 3 * D.d + 2 * D.d + h * kDh + c;
     const int64_t ld = 3 * (int64_t)D.d;
     float m = 0.0f;
     for (int i = lane; i < D.t; i += 64) m = fmaxf(m, fabsf(col[i * ld]));
     m = wave_max(m);
     const float s = m == 0.0f ? 1.0f : m / 127.0f;
     const float inv = 1.0f / s;
-    int8_t *dst = W.vq + ((int64_t)h * kDh + c) * D.tv;
+    int8_t *dst = W.vq + ((int64_t)item) * D.tv;
     for (int i = lane; i < D.tv; i += 64) dst[i] = i < D.t ? q_code(col[i * ld], inv) : (int8_t)0;
-    if (lane == 0) W.vs[h * kDh + c] = s;
+    if (lane == 0) W.vs[item] = s;
 }
 
 // LDS plan of attn_core_kernel (bytes): s1 [16][s1w] f32, s2 [16][s2w] f32, pq [16][tv] int8, row stats.
@@ -148,6 +153,19 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.y, i0 = blockIdx.x * 16;
     const int t = D.t;
+    // segment blockIdx.z: its per-token tables and its rows of ctx (the relative rows are shared)
+    {
+        const int64_t seg = blockIdx.z, so = seg * D.h * D.tp;
+        W.qu += so * kDh;
+        W.qv += so * kDh;
+        W.kq += so * kDh;
+        W.qus += so;
+        W.qvs += so;
+        W.ks += so;
+        W.vq += seg * D.h * kDh * D.tv;
+        W.vs += seg * D.h * kDh;
+        ctx += seg * D.t * D.d;
+    }
     const int imax = min(i0 + 15, t - 1);
     const int pb0 = (t - 1 - imax) & ~15;        // first position block of the band
     const int pend = 2 * t - 2 - i0;             // last position used by the block
@@ -272,53 +290,59 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
     }
 }
 
-size_t attn_ws_bytes(int64_t t, int64_t d, int64_t h) {
+size_t attn_ws_bytes_seg(int64_t t, int64_t d, int64_t h, int64_t nseg) {
     const AttnDims D((int)t, (int)d, (int)h);
-    const size_t rows = (size_t)h * D.tp, rrows = (size_t)h * D.rp;
+    const size_t rows = (size_t)(nseg * h) * D.tp, rrows = (size_t)h * D.rp;
     size_t b = 0;
     auto add = [&](size_t n) { b += (n + 255) / 256 * 256; };
     add(rows * kDh);       // qu
     add(rows * kDh);       // qv
     add(rows * kDh);       // kq
     add(rrows * kDh);      // rq
-    add((size_t)h * kDh * D.tv);  // vq
+    add((size_t)(nseg * h) * kDh * D.tv);  // vq
     add(rows * 4);         // qus
     add(rows * 4);         // qvs
     add(rows * 4);         // ks
     add(rrows * 4);        // rs
-    add((size_t)h * kDh * 4);     // vs
+    add((size_t)(nseg * h) * kDh * 4);     // vs
     return b;
 }
 
-// ctx [t][d] from qkv [t][3d] (q | k | v) and rel_k [2t-1][d]; ws is attn_ws_bytes(t, d, h) device bytes.
-void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h, const float *bias_u,
-                    const float *bias_v, float scaling, void *ws, float *ctx, hipStream_t st) {
+size_t attn_ws_bytes(int64_t t, int64_t d, int64_t h) { return attn_ws_bytes_seg(t, d, h, 1); }
+
+// ctx [nseg][t][d] from qkv [nseg][t][3d] (q | k | v) and the shared rel_k [2t-1][d] of t frames: each segment's
+// attention on its own tokens; ws is attn_ws_bytes_seg(t, d, h, nseg) device bytes.
+void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
+                        const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
+                        hipStream_t st) {
     require(qkv && rel_k && bias_u && bias_v && ws && ctx, "attention: NULL pointer");
     require(h > 0 && d == h * kDh, "attention: the head dimension must be 128");
     require(t >= 1 && t <= 1024, "attention: 1 <= t <= 1024 frames");
-    const AttnDims D((int)t, (int)d, (int)h);
+    require(nseg >= 1 && nseg <= 65535 && nseg * t * 3 * d < (1ll << 31), "attention: 1 <= segments, size < 2^31");
+    AttnDims D((int)t, (int)d, (int)h);
+    D.nseg = (int)nseg;
     uint8_t *p = (uint8_t *)ws;
     auto take = [&](size_t n) {
         uint8_t *r = p;
         p += (n + 255) / 256 * 256;
         return r;
     };
-    const size_t rows = (size_t)h * D.tp, rrows = (size_t)h * D.rp;
+    const size_t rows = (size_t)(nseg * h) * D.tp, rrows = (size_t)h * D.rp;
     AttnWs W;
     W.qu = (int8_t *)take(rows * kDh);
     W.qv = (int8_t *)take(rows * kDh);
     W.kq = (int8_t *)take(rows * kDh);
     W.rq = (int8_t *)take(rrows * kDh);
-    W.vq = (int8_t *)take((size_t)h * kDh * D.tv);
+    W.vq = (int8_t *)take((size_t)(nseg * h) * kDh * D.tv);
     W.qus = (float *)take(rows * 4);
     W.qvs = (float *)take(rows * 4);
     W.ks = (float *)take(rows * 4);
     W.rs = (float *)take(rrows * 4);
-    W.vs = (float *)take((size_t)h * kDh * 4);
+    W.vs = (float *)take((size_t)(nseg * h) * kDh * 4);
     const int items = (int)(rows + rrows);
     attn_rows_kernel<<<(unsigned)((items + 3) / 4), 256, 0, st>>>(qkv, rel_k, bias_u, bias_v, D, W);
     hip_check(hipGetLastError(), "attention rows kernel launch");
-    attn_vt_kernel<<<(unsigned)((h * kDh + 3) / 4), 256, 0, st>>>(qkv, D, W);
+    attn_vt_kernel<<<(unsigned)((nseg * h * kDh + 3) / 4), 256, 0, st>>>(qkv, D, W);
     hip_check(hipGetLastError(), "attention vT kernel launch");
     const size_t lds = core_lds_bytes((int)t);
     static bool lds_raised = false;
@@ -328,8 +352,15 @@ void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, 
                   "attention LDS limit");
         lds_raised = true;
     }
-    attn_core_kernel<<<dim3((unsigned)(D.tp / 16), (unsigned)h), 256, lds, st>>>(D, W, scaling, ctx);
+    attn_core_kernel<<<dim3((unsigned)(D.tp / 16), (unsigned)h, (unsigned)nseg), 256, lds, st>>>(D, W, scaling,
+                                                                                                    ctx);
     hip_check(hipGetLastError(), "attention core kernel launch");
+}
+
+// ctx [t][d] from qkv [t][3d] (q | k | v) and rel_k [2t-1][d]; ws is attn_ws_bytes(t, d, h) device bytes.
+void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h, const float *bias_u,
+                    const float *bias_v, float scaling, void *ws, float *ctx, hipStream_t st) {
+    attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, ws, ctx, st);
 }
 
 }  // namespace vx

@@ -33,20 +33,21 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
 void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const float *g, const float *b, int8_t *q,
                  float *scales_t, int32_t *gsum_t, hipStream_t stream);
 void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y, hipStream_t stream);
-void glu_dwconv_silu(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t, const float *bias, float *out,
-                     hipStream_t st);
-int64_t subsampling(const float *feats, int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s, const float *conv0_w,
-                    const float *conv0_b, const float *dw_w, const float *dw_b, const float *pw_w, const float *pw_b,
-                    const float *lin_w, const float *lin_b, int64_t d_model, float *scratch, float *out,
-                    hipStream_t st);
+void glu_dwconv_silu_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
+                         const float *bias, float *out, hipStream_t st);
+int64_t subsampling_seg(const float *feats, int64_t nseg, int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s,
+                        const float *conv0_w, const float *conv0_b, const float *dw_w, const float *dw_b,
+                        const float *pw_w, const float *pw_b, const float *lin_w, const float *lin_b,
+                        int64_t d_model, float *scratch, float *out, hipStream_t st);
 int64_t subsampling_frames(int64_t t, int64_t k, int64_t s);
 int64_t subsampling_scratch_floats(int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s);
 void fold_bn(const float *dw, const float *gamma, const float *beta, const float *mean, const float *var, int64_t d,
              int64_t k, float *dw_t, float *dw_bias);
 void rel_pos_table(int64_t t, int64_t d, float *out);
-size_t attn_ws_bytes(int64_t t, int64_t d, int64_t h);
-void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h, const float *bias_u,
-                    const float *bias_v, float scaling, void *ws, float *ctx, hipStream_t st);
+size_t attn_ws_bytes_seg(int64_t t, int64_t d, int64_t h, int64_t nseg);
+void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
+                        const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
+                        hipStream_t st);
 
 namespace {
 
@@ -105,8 +106,8 @@ struct EncLayer {
     }
 };
 
-struct EncWs {  // everything one forward of t frames touches
-    int64_t t = 0, np = 0;
+struct EncWs {  // everything one forward of nseg segments of t frames touches
+    int64_t t = 0, nseg = 1, np = 0;
     DevBuf x[2], hbuf, qkv, rel_k, ctx, g2, hb, pos, attn, sub_scratch, feats;
     QBuf a, f, posq;
     int64_t t_in = 0;
@@ -125,7 +126,7 @@ struct vx_encoder {
     vx::DevBuf sub_w[8];
     bool sub_set = false;
     bool graphs = true;
-    std::map<int64_t, std::unique_ptr<vx::EncWs>> ws;  // by frame count
+    std::map<std::pair<int64_t, int64_t>, std::unique_ptr<vx::EncWs>> ws;  // by (frames, segments)
 };
 
 namespace vx {
@@ -144,24 +145,28 @@ int64_t dim_of(const vx_encoder_config &c, int code) {
     }
 }
 
-EncWs &workspace(vx_encoder *e, int64_t t) {
-    auto it = e->ws.find(t);
+// Workspace of nseg segments of t frames: the token-row buffers hold nseg * t rows; the relative position table,
+// its projection and the quantized table depend on t only and are shared by the segments.
+EncWs &workspace(vx_encoder *e, int64_t t, int64_t nseg) {
+    auto it = e->ws.find({t, nseg});
     if (it != e->ws.end()) return *it->second;
     const vx_encoder_config &c = e->cfg;
     auto w = std::make_unique<EncWs>();
     w->t = t;
+    w->nseg = nseg;
     w->np = 2 * t - 1;
+    const int64_t n = nseg * t;
     const size_t f4 = sizeof(float);
-    for (auto &x : w->x) x = DevBuf((size_t)(t * c.d) * f4);
-    w->hbuf = DevBuf((size_t)(t * c.ff) * f4);
-    w->qkv = DevBuf((size_t)(t * 3 * c.d) * f4);
+    for (auto &x : w->x) x = DevBuf((size_t)(n * c.d) * f4);
+    w->hbuf = DevBuf((size_t)(n * c.ff) * f4);
+    w->qkv = DevBuf((size_t)(n * 3 * c.d) * f4);
     w->rel_k = DevBuf((size_t)(w->np * c.d) * f4);
-    w->ctx = DevBuf((size_t)(t * c.d) * f4);
-    w->g2 = DevBuf((size_t)(t * 2 * c.d) * f4);
-    w->hb = DevBuf((size_t)(t * c.d) * f4);
-    w->attn = DevBuf(attn_ws_bytes(t, c.d, c.heads));
-    w->a.alloc(t, c.d, c.group);
-    w->f.alloc(t, c.ff, c.group);
+    w->ctx = DevBuf((size_t)(n * c.d) * f4);
+    w->g2 = DevBuf((size_t)(n * 2 * c.d) * f4);
+    w->hb = DevBuf((size_t)(n * c.d) * f4);
+    w->attn = DevBuf(attn_ws_bytes_seg(t, c.d, c.heads, nseg));
+    w->a.alloc(n, c.d, c.group);
+    w->f.alloc(n, c.ff, c.group);
     w->posq.alloc(w->np, c.d, c.group);
     // the relative position table of t frames, quantized once (its quantization is input-independent)
     std::vector<float> pos((size_t)(w->np * c.d));
@@ -171,7 +176,7 @@ EncWs &workspace(vx_encoder *e, int64_t t) {
                 w->posq.s.as<float>(), w->posq.g.as<int32_t>(), nullptr);
     hip_check(hipDeviceSynchronize(), "position table quantization");
     EncWs &ref = *w;
-    e->ws[t] = std::move(w);
+    e->ws[{t, nseg}] = std::move(w);
     return ref;
 }
 
@@ -180,10 +185,11 @@ void gemm_full(const vx_tmat *w, const QBuf &a, int64_t n, float *y, int ep, flo
          0, n, st);
 }
 
-// The layer stack on ws.x[0] (result in ws.x[n_layers % 2]).
+// The layer stack on ws.x[0] (result in ws.x[n_layers % 2]). The token-row work runs over all nseg * t rows at
+// once; the depthwise convolution and the attention stay inside each segment.
 void run_layers(vx_encoder *e, EncWs &w, hipStream_t st) {
     const vx_encoder_config &c = e->cfg;
-    const int64_t t = w.t, d = c.d, G = c.group;
+    const int64_t t = w.nseg * w.t, d = c.d, G = c.group;
     const float scaling = 1.0f / std::sqrt((float)(d / c.heads));
     for (size_t li = 0; li < e->layers.size(); li++) {
         EncLayer &L = *e->layers[li];
@@ -207,15 +213,15 @@ void run_layers(vx_encoder *e, EncWs &w, hipStream_t st) {
         lnq(1);
         gemm_full(L.lin[2], w.a, t, w.qkv.as<float>(), VX_EP_STORE, 0.0f, st);
         gemm_full(L.lin[4], w.posq, w.np, w.rel_k.as<float>(), VX_EP_STORE, 0.0f, st);
-        attention_core(w.qkv.as<float>(), w.rel_k.as<float>(), t, d, c.heads, L.bias_u.as<float>(),
-                       L.bias_v.as<float>(), scaling, w.attn.p, w.ctx.as<float>(), st);
+        attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>(), w.nseg, w.t, d, c.heads, L.bias_u.as<float>(),
+                           L.bias_v.as<float>(), scaling, w.attn.p, w.ctx.as<float>(), st);
         quant(w.ctx.as<float>(), d, w.a);
         gemm_full(L.lin[3], w.a, t, x, VX_EP_ADD_SCALED, 1.0f, st);
         // convolution module
         lnq(2);
         gemm_full(L.lin[5], w.a, t, w.g2.as<float>(), VX_EP_STORE, 0.0f, st);
-        glu_dwconv_silu(w.g2.as<float>(), t, d, c.kconv, L.dw_t.as<float>(), L.dw_bias.as<float>(), w.hb.as<float>(),
-                        st);
+        glu_dwconv_silu_seg(w.g2.as<float>(), w.nseg, w.t, d, c.kconv, L.dw_t.as<float>(), L.dw_bias.as<float>(),
+                            w.hb.as<float>(), st);
         quant(w.hb.as<float>(), d, w.a);
         gemm_full(L.lin[6], w.a, t, x, VX_EP_ADD_SCALED, 1.0f, st);
         ffn(3, 7, 8);
@@ -228,12 +234,13 @@ void check_ready(const vx_encoder *e) {
         if (!e->layers[i]->set) throw Error(VX_ERR_INVALID, "encoder layer " + std::to_string(i) + " has no weights");
 }
 
-// x (device [t][d]) -> the encoder output (device [t][d]), both caller buffers (they may alias).
-void forward_layers(vx_encoder *e, const float *x_in, float *x_out, int64_t t, hipStream_t st) {
+// x (device [nseg][t][d]) -> the encoder output (device [nseg][t][d]), both caller buffers (they may alias).
+void forward_layers(vx_encoder *e, const float *x_in, float *x_out, int64_t t, int64_t nseg, hipStream_t st) {
     check_ready(e);
     require(t >= 1 && t <= 1024, "encoder: 1 <= t <= 1024 frames");
-    EncWs &w = workspace(e, t);
-    const size_t bytes = (size_t)(t * e->cfg.d) * sizeof(float);
+    require(nseg >= 1 && nseg * t <= 65535, "encoder: 1 <= segments, segments * t <= 65535");
+    EncWs &w = workspace(e, t, nseg);
+    const size_t bytes = (size_t)(nseg * t * e->cfg.d) * sizeof(float);
     hip_check(hipMemcpyAsync(w.x[0].p, x_in, bytes, hipMemcpyDeviceToDevice, st), "encoder input copy");
     if (e->graphs && st != nullptr) {  // the legacy NULL stream cannot be captured
         if (!w.exec || w.exec_stream != st) {
@@ -341,30 +348,40 @@ void encoder_set_subsampling(vx_encoder *e, const vx_subsampling_params *p) {
     e->sub_set = true;
 }
 
-void encoder_forward_feats(vx_encoder *e, const float *feats, int64_t t_in, float *out, int64_t *t_out,
-                           hipStream_t st) {
+void encoder_forward_feats_batch(vx_encoder *e, const float *feats, int64_t nseg, int64_t t_in, float *out,
+                                 int64_t *t_out, hipStream_t st) {
     require(e && feats && out, "NULL argument");
     require(e->sub_set, "encoder: subsampling weights not set");
     const vx_encoder_config &c = e->cfg;
     const int64_t t = subsampling_frames(t_in, c.sub_kernel, c.sub_stride);
     require(t >= 1 && t <= 1024, "encoder: 1 <= subsampled frames <= 1024");
-    EncWs &w = workspace(e, t);
+    require(nseg >= 1 && nseg * t <= 65535, "encoder: 1 <= segments, segments * frames <= 65535");
+    EncWs &w = workspace(e, t, nseg);
     const int64_t scratch = subsampling_scratch_floats(t_in, c.n_mels, c.sub_channels, c.sub_kernel, c.sub_stride);
     if (w.t_in < t_in) {
-        w.sub_scratch = DevBuf((size_t)scratch * sizeof(float));
+        w.sub_scratch = DevBuf((size_t)(nseg * scratch) * sizeof(float));
         w.t_in = t_in;
     }
-    subsampling(feats, t_in, c.n_mels, c.sub_channels, c.sub_kernel, c.sub_stride, e->sub_w[0].as<float>(),
-                e->sub_w[1].as<float>(), e->sub_w[2].as<float>(), e->sub_w[3].as<float>(), e->sub_w[4].as<float>(),
-                e->sub_w[5].as<float>(), e->sub_w[6].as<float>(), e->sub_w[7].as<float>(), c.d,
-                w.sub_scratch.as<float>(), out, st);
-    forward_layers(e, out, out, t, st);
+    subsampling_seg(feats, nseg, t_in, c.n_mels, c.sub_channels, c.sub_kernel, c.sub_stride, e->sub_w[0].as<float>(),
+                    e->sub_w[1].as<float>(), e->sub_w[2].as<float>(), e->sub_w[3].as<float>(),
+                    e->sub_w[4].as<float>(), e->sub_w[5].as<float>(), e->sub_w[6].as<float>(),
+                    e->sub_w[7].as<float>(), c.d, w.sub_scratch.as<float>(), out, st);
+    forward_layers(e, out, out, t, nseg, st);
     if (t_out) *t_out = t;
 }
 
-void encoder_forward(vx_encoder *e, const float *x, float *out, int64_t t, hipStream_t st) {
+void encoder_forward_feats(vx_encoder *e, const float *feats, int64_t t_in, float *out, int64_t *t_out,
+                           hipStream_t st) {
+    encoder_forward_feats_batch(e, feats, 1, t_in, out, t_out, st);
+}
+
+void encoder_forward_batch(vx_encoder *e, const float *x, float *out, int64_t nseg, int64_t t, hipStream_t st) {
     require(e && x && out, "NULL argument");
-    forward_layers(e, x, out, t, st);
+    forward_layers(e, x, out, t, nseg, st);
+}
+
+void encoder_forward(vx_encoder *e, const float *x, float *out, int64_t t, hipStream_t st) {
+    encoder_forward_batch(e, x, out, 1, t, st);
 }
 
 }  // namespace vx

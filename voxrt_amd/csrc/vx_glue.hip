@@ -21,32 +21,43 @@ namespace vx {
 // out[i][c] = silu(bias[c] + sum over taps kk of w[kk][c] * glu(g[i + kk - pad][c])), taps outside [0, t) skipped,
 // each product and sum rounded separately (encoder.rs:604-624). g is the pointwise_conv1 output [t][2d]; the GLU
 // value of a tap is recomputed per output (it is a pure function of g), so no [t][d] intermediate is stored.
+// Row blockIdx.y of [nseg][t] rows: the taps stay inside its segment (rows outside are the zero padding).
 __global__ __launch_bounds__(256) void glu_dwconv_silu_kernel(const float *__restrict__ g, int t, int d, int k,
                                                              const float *__restrict__ w_t,
                                                              const float *__restrict__ bias, float *__restrict__ out) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    const int i = blockIdx.y;
+    const int row = blockIdx.y, i = row % t, base = row - i;
     if (c >= d) return;
     const int pad = (k - 1) / 2;
     float acc = bias[c];
     for (int kk = 0; kk < k; kk++) {
         const int j = i + kk - pad;
         if (j < 0 || j >= t) continue;
-        const float *gj = g + (int64_t)j * 2 * d;
+        const float *gj = g + (int64_t)(base + j) * 2 * d;
         const float a = gj[c] * sigmoid_fast(gj[d + c]);
         acc = acc + w_t[(int64_t)kk * d + c] * a;
     }
-    out[(int64_t)i * d + c] = silu_fast(acc);
+    out[(int64_t)row * d + c] = silu_fast(acc);
+}
+
+// nseg segments of t frames each: g [nseg][t][2d] -> out [nseg][t][d].
+void glu_dwconv_silu_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
+                         const float *bias, float *out, hipStream_t st) {
+    require(g && w_t && bias && out, "glu_dwconv: NULL pointer");
+    require(nseg >= 1 && t >= 0 && d > 0 && k > 0 && k % 2 == 1 && nseg * t * 2 * d < (1ll << 31) &&
+                nseg * t <= 65535,
+            "glu_dwconv: bad shape");
+    if (t == 0) return;
+    glu_dwconv_silu_kernel<<<dim3((unsigned)((d + 255) / 256), (unsigned)(nseg * t)), 256, 0, st>>>(
+        g, (int)t, (int)d, (int)k, w_t, bias, out);
+    hip_check(hipGetLastError(), "glu_dwconv kernel launch");
 }
 
 void glu_dwconv_silu(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t, const float *bias, float *out,
                      hipStream_t st) {
-    require(g && w_t && bias && out, "glu_dwconv: NULL pointer");
-    require(t >= 0 && d > 0 && k > 0 && k % 2 == 1 && t * 2 * d < (1ll << 31), "glu_dwconv: bad shape");
+    require(t <= 65535, "glu_dwconv: t <= 65535");
     if (t == 0) return;
-    glu_dwconv_silu_kernel<<<dim3((unsigned)((d + 255) / 256), (unsigned)t), 256, 0, st>>>(g, (int)t, (int)d, (int)k,
-                                                                                          w_t, bias, out);
-    hip_check(hipGetLastError(), "glu_dwconv kernel launch");
+    glu_dwconv_silu_seg(g, 1, t, d, k, w_t, bias, out, st);
 }
 
 // ---------------------------------------------------------------------------------------- f32 linear
@@ -188,7 +199,9 @@ __global__ __launch_bounds__(256) void conv0_kernel(const float *__restrict__ fe
                                                    const float *__restrict__ w, const float *__restrict__ b, int c,
                                                    int t1, int f1, float *__restrict__ out) {
     __shared__ float rows[kMaxK][kMaxMels];
-    const int ot = blockIdx.x, p = (k - 1) / 2;
+    const int ot = blockIdx.x % t1, seg = blockIdx.x / t1, p = (k - 1) / 2;
+    feats += (int64_t)seg * t * nm;  // segment seg of [nseg][t][nm] -> [nseg][t1][f1][c]
+    out += (int64_t)seg * t1 * f1 * c;
     for (int e = threadIdx.x; e < k * nm; e += blockDim.x) {
         const int kt = e / nm, f = e % nm, it = ot * s + kt - p;
         rows[kt][f] = (it >= 0 && it < t) ? feats[(int64_t)it * nm + f] : 0.0f;
@@ -227,8 +240,10 @@ __global__ __launch_bounds__(256) void conv0_kernel(const float *__restrict__ fe
 __global__ __launch_bounds__(256) void dwconv2d_kernel(const float *__restrict__ x, int tc, int fc, int k, int s,
                                                       const float *__restrict__ w, const float *__restrict__ b, int c,
                                                       int t2, int f2, float *__restrict__ y) {
-    const int pos = blockIdx.x;
+    const int seg = blockIdx.x / (t2 * f2), pos = blockIdx.x % (t2 * f2);
     const int ot = pos / f2, of = pos % f2, p = (k - 1) / 2;
+    x += (int64_t)seg * tc * fc * c;  // segment seg of [nseg][tc][fc][c] -> [nseg][t2][f2][c]
+    y += (int64_t)seg * t2 * f2 * c;
     for (int ch = threadIdx.x; ch < c; ch += blockDim.x) {
         float o = b[ch];
         for (int kt = 0; kt < k; kt++) {
@@ -244,37 +259,45 @@ __global__ __launch_bounds__(256) void dwconv2d_kernel(const float *__restrict__
     }
 }
 
-// The whole subsampling (subsampling.rs:124-204) on device buffers; scratch must hold 2 * t1 * f1 * c floats.
-// Returns the output frame count; out is [t3][d_model].
-int64_t subsampling(const float *feats, int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s, const float *conv0_w,
-                    const float *conv0_b, const float *dw_w, const float *dw_b, const float *pw_w, const float *pw_b,
-                    const float *lin_w, const float *lin_b, int64_t d_model, float *scratch, float *out,
-                    hipStream_t st) {
+// The whole subsampling (subsampling.rs:124-204) of nseg segments of t frames each on device buffers: feats
+// [nseg][t][nm] -> out [nseg][t3][d_model]; scratch must hold 2 * nseg * t1 * f1 * c floats. Returns t3.
+int64_t subsampling_seg(const float *feats, int64_t nseg, int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s,
+                        const float *conv0_w, const float *conv0_b, const float *dw_w, const float *dw_b,
+                        const float *pw_w, const float *pw_b, const float *lin_w, const float *lin_b,
+                        int64_t d_model, float *scratch, float *out, hipStream_t st) {
     require(feats && conv0_w && conv0_b && dw_w && dw_b && pw_w && pw_b && lin_w && lin_b && scratch && out,
             "subsampling: NULL pointer");
     require(t > 0 && nm > 0 && nm <= kMaxMels && c > 0 && k > 0 && k <= kMaxK && s > 0 && c <= 1024,
             "subsampling: bad shape (k <= 3, n_mels <= 256)");
     const int p = (int)(k - 1) / 2;
     const int t1 = conv_out_len((int)t, (int)k, (int)s, p), f1 = conv_out_len((int)nm, (int)k, (int)s, p);
-    require((int64_t)t1 * f1 * c < (1ll << 31), "subsampling: input too long");
-    float *a = scratch, *bbuf = scratch + (int64_t)t1 * f1 * c;
-    conv0_kernel<<<(unsigned)t1, 256, 0, st>>>(feats, (int)t, (int)nm, (int)k, (int)s, conv0_w,
+    require(nseg >= 1 && nseg * t1 * f1 * c < (1ll << 31), "subsampling: input too long");
+    float *a = scratch, *bbuf = scratch + nseg * t1 * f1 * c;
+    conv0_kernel<<<(unsigned)(nseg * t1), 256, 0, st>>>(feats, (int)t, (int)nm, (int)k, (int)s, conv0_w,
                                                                 conv0_b, (int)c, t1, f1, a);
     hip_check(hipGetLastError(), "conv0 kernel launch");
     int tc = t1, fc = f1;
     for (int stage = 0; stage < 2; stage++) {
         const int t2 = conv_out_len(tc, (int)k, (int)s, p), f2 = conv_out_len(fc, (int)k, (int)s, p);
-        dwconv2d_kernel<<<(unsigned)(t2 * f2), 256, 0, st>>>(a, tc, fc, (int)k, (int)s,
+        dwconv2d_kernel<<<(unsigned)(nseg * t2 * f2), 256, 0, st>>>(a, tc, fc, (int)k, (int)s,
                                                                       dw_w + (int64_t)stage * k * k * c,
                                                                       dw_b + (int64_t)stage * c, (int)c, t2, f2, bbuf);
         hip_check(hipGetLastError(), "dwconv2d kernel launch");
-        linear_f32(bbuf, (int64_t)t2 * f2, c, pw_w + (int64_t)stage * c * c, pw_b + (int64_t)stage * c, c, a, true,
+        linear_f32(bbuf, nseg * t2 * f2, c, pw_w + (int64_t)stage * c * c, pw_b + (int64_t)stage * c, c, a, true,
                    st);
         tc = t2;
         fc = f2;
     }
-    linear_f32(a, tc, (int64_t)fc * c, lin_w, lin_b, d_model, out, false, st);
+    linear_f32(a, nseg * tc, (int64_t)fc * c, lin_w, lin_b, d_model, out, false, st);
     return tc;
+}
+
+int64_t subsampling(const float *feats, int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s, const float *conv0_w,
+                    const float *conv0_b, const float *dw_w, const float *dw_b, const float *pw_w, const float *pw_b,
+                    const float *lin_w, const float *lin_b, int64_t d_model, float *scratch, float *out,
+                    hipStream_t st) {
+    return subsampling_seg(feats, 1, t, nm, c, k, s, conv0_w, conv0_b, dw_w, dw_b, pw_w, pw_b, lin_w, lin_b, d_model,
+                           scratch, out, st);
 }
 
 int64_t subsampling_frames(int64_t t, int64_t k, int64_t s) {

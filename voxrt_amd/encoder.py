@@ -276,6 +276,29 @@ class Encoder:
                                              K._stream()))
         return out
 
+    def forward_batch(self, x, out=None):
+        """The layer stack on nseg segments of equal length at once: x [nseg, t, d] -> out [nseg, t, d]; each
+        segment's output equals forward() of that segment alone, bit for bit."""
+        import torch
+
+        nseg, t = x.shape[0], x.shape[1]
+        out = torch.empty_like(x) if out is None else out
+        check(lib().vx_encoder_forward_batch(self._h, _f32(x, "x"), _f32(out, "out"), nseg, t, K._stream()))
+        return out
+
+    def forward_feats_batch(self, feats, out=None):
+        """Subsampling + layers on nseg segments of equal length: feats [nseg, t_in, n_mels] -> [nseg, t_out, d],
+        each segment equal to forward_feats() of that segment alone."""
+        import torch
+
+        nseg, t_in = feats.shape[0], feats.shape[1]
+        t3 = self.out_frames(t_in)
+        out = torch.empty((nseg, t3, self.d), dtype=torch.float32, device=feats.device) if out is None else out
+        got = C.c_int64()
+        check(lib().vx_encoder_forward_feats_batch(self._h, _f32(feats, "feats"), nseg, t_in, _f32(out, "out"),
+                                                   C.byref(got), K._stream()))
+        return out
+
     def free(self) -> None:
         if self._h is not None and self._h.value:
             lib().vx_encoder_free(self._h)

@@ -79,6 +79,8 @@ def lib() -> C.CDLL:
             "vx_encoder_use_graphs": (I, [P, I]),
             "vx_encoder_forward": (I, [P, P, P, I64, P]),
             "vx_encoder_forward_feats": (I, [P, P, I64, P, C.POINTER(I64), P]),
+            "vx_encoder_forward_batch": (I, [P, P, P, I64, I64, P]),
+            "vx_encoder_forward_feats_batch": (I, [P, P, I64, I64, P, C.POINTER(I64), P]),
             "vx_encoder_free": (None, [P]),
         }
         for name, (res, args) in sig.items():
