@@ -422,3 +422,41 @@ def test_stream_kernel_every_output(dev, orc, m, k, n_out, grid):
                 os.environ.pop(v, None)
             else:
                 os.environ[v] = val
+
+
+@pytest.mark.parametrize("m,k,n_out,grid", [(1536, 1024, 2048, 16), (1536 + 37, 1024, 1024, 8),
+                                            (1024, 4096, 1024, 8), (2048, 1024, 3072, 0)])
+def test_stream_groups_kernel_every_output(dev, orc, m, k, n_out, grid):
+    """The streaming kernel for 128-column groups (the model format: f16 scales per row and group, per-token and
+    group activation scales), forced on shapes the oracle checks in full: several tiles per workgroup, K = 4096
+    (32 groups), a ragged token count whose last 37 rows go through another kernel; each epilogue with and without
+    bias, every output bit-exact."""
+    import voxrt_amd as vx
+
+    group = 128
+    trits, s16, x = _workload(orc, m, k, n_out, group, seed_cfg=6)
+    ws = orc.f16_to_f32(s16)
+    w = vx.TernaryMatrix.from_packed(synth.pack_rows(trits), s16, n_out, k, group)
+    q, xs, _ = orc.quantize(x, group)
+    xa = vx.QuantAct.quantize(_t(x, dev), group)
+    rng = synth.Lcg(43)
+    base = ((rng.take(m * n_out) % 200).astype(np.float32) * np.float32(0.01) - np.float32(1.0)).reshape(m, n_out)
+    bias = (rng.take(n_out) % 100).astype(np.float32) / np.float32(10.0)
+    old = {v: os.environ.get(v) for v in ("VX_GEMM", "VX_STREAM_GRID")}
+    os.environ["VX_GEMM"] = "stream"
+    os.environ["VX_STREAM_GRID"] = str(grid)
+    try:
+        for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
+            want = orc.gemm(trits, ws, q, xs, group, y=base.copy(), ep=ep_kind, alpha=alpha)
+            for with_bias in (False, True):
+                y = _t(base, dev)
+                vx.gemm_ep(w, xa, y, _t(bias, dev) if with_bias else None, _ep_of(vx, ep_kind, alpha))
+                exp = (want + bias[None, :]).astype(np.float32) if with_bias else want
+                _assert_bits_equal(y.cpu().numpy(), exp, f"stream groups {m}x{k}x{n_out} grid={grid} "
+                                                         f"ep={ep_kind} bias={with_bias}")
+    finally:
+        for v, val in old.items():
+            if val is None:
+                os.environ.pop(v, None)
+            else:
+                os.environ[v] = val

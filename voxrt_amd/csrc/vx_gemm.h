@@ -2,6 +2,8 @@
 // vx_gemm_stream.hip).
 #pragma once
 
+#include <type_traits>
+
 #include "vx_internal.h"
 
 namespace vx {
@@ -32,8 +34,37 @@ __device__ inline v4i widen_codes(uint32_t p) {
     return r;
 }
 
-// Streaming large-token kernel (vx_gemm_stream.hip): runs the GEMM and returns true when the shape and window
-// fit it (whole 128-token x 256-row tiles, one group, ternary weights), else returns false and launches nothing.
+// --- streaming large-token kernels (vx_gemm_stream.hip: one group; vx_gemm_stream_g.hip: 128-column groups) ---
+
+constexpr int kBM = 128, kBN = 256;  // workgroup tile: tokens x output rows
+constexpr uint32_t kOff = 0xFFFFFFF0u;
+
+struct StreamGeom {
+    int n_nt;     // tiles along the output rows
+    int ntiles;   // tiles in all
+    int per_xcd;  // tiles per XCD (a contiguous range of the tile order)
+    int nk;       // 64-column K steps (a multiple of 8, at least 16)
+    int ng;       // groups
+};
+
+// s_waitcnt immediate on gfx9: vmcnt in bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left unwaited.
+constexpr int waitcnt_vm(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+template <int I>
+using IC = std::integral_constant<int, I>;
+
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(IC<B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// The streaming kernels run the GEMM and return true when the shape and window fit them (whole 128-token x
+// 256-row tiles of a full-width ternary GEMM), else return false and launch nothing.
 bool gemm_stream(const GemmArgs &a, int tokens_full, hipStream_t st);
+bool gemm_stream_groups(const GemmArgs &a, int tokens_full, hipStream_t st);
+int cu_count();  // compute units of the current device
 
 }  // namespace vx

@@ -1291,11 +1291,11 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
     a.ep = ep;
     a.alpha = alpha;
     const bool tern = w->ternary, g = gs != nullptr, single = w->ng == 1;
-    // whole 128-token tiles of a full-width single-group ternary GEMM: the streaming kernel; the remaining tokens
-    // (fewer than 128) go through the kernels below
-    if (tern && single && !g && r0 == 0 && r1 == w->out && t0 == 0 && n >= 128) {
+    // whole 128-token tiles of a full-width ternary GEMM (one group or 128-column groups): the streaming kernels;
+    // the remaining tokens (fewer than 128) go through the kernels below
+    if (tern && !g && r0 == 0 && r1 == w->out && t0 == 0 && n >= 128) {
         const int64_t full = n / 128 * 128;
-        if (full < (1ll << 30) && gemm_stream(a, (int)full, st)) {
+        if (full < (1ll << 30) && (single ? gemm_stream(a, (int)full, st) : gemm_stream_groups(a, (int)full, st))) {
             if (full == n) return;
             a.t0 = full;
             a.m_base = full;

@@ -42,30 +42,6 @@
 namespace vx {
 namespace {
 
-constexpr int kBM = 128, kBN = 256;  // workgroup tile: tokens x output rows
-constexpr uint32_t kOff = 0xFFFFFFF0u;
-
-struct StreamGeom {
-    int n_nt;     // tiles along the output rows
-    int ntiles;   // tiles in all
-    int per_xcd;  // tiles per XCD (a contiguous range of the tile order)
-    int nk;       // 64-column K steps (a multiple of 8, at least 16)
-};
-
-// s_waitcnt immediate on gfx9: vmcnt in bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left unwaited.
-constexpr int waitcnt_vm(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (15 << 8); }
-
-template <int I>
-using IC = std::integral_constant<int, I>;
-
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-    if constexpr (B < E) {
-        f(IC<B>{});
-        static_for<B + 1, E>(f);
-    }
-}
-
 // Loads run kPD steps ahead of use. When step s begins, the loads of step s+1 (the first instructions of step
 // s+1-kPD) must be complete: the vector-memory instructions issued after them are 2 stores of that step and 5 per
 // later step (3 DMA + 2 stores), plus the 4 scale DMAs issued after the loads of tile step nk-kPD.
@@ -396,6 +372,8 @@ void launch_stream(const GemmArgs &a, const StreamGeom &g, int grid, hipStream_t
         tgemm_stream_kernel<EP, BIAS, false><<<grid, 256, 0, st>>>(a, g);
 }
 
+}  // namespace
+
 int cu_count() {
     static int n = 0;
     if (n == 0) {
@@ -407,8 +385,6 @@ int cu_count() {
     }
     return n;
 }
-
-}  // namespace
 
 bool gemm_stream(const GemmArgs &a, int tokens_full, hipStream_t st) {
     const int64_t nk = a.inp / 64;
@@ -422,6 +398,7 @@ bool gemm_stream(const GemmArgs &a, int tokens_full, hipStream_t st) {
     g.ntiles = (tokens_full / kBM) * g.n_nt;
     g.per_xcd = (g.ntiles + 7) / 8;
     g.nk = (int)nk;
+    g.ng = 1;
     const int cus = cu_count();
     if (g.ntiles < cus && !(kv && *kv)) return false;  // too few tiles to fill the chip: the other kernels
     int per_x = std::min(cus / 8, g.per_xcd);
