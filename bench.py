@@ -391,7 +391,7 @@ def main():
     per = time_launches(torch, gemms, 20)
     dom = max(gemms, key=lambda g: per[g.name])
     roof = roofline_of(dom, per[dom.name])
-    roof["kernel"] = f"ternary GEMM {dom.name}: M={dom.m} K={dom.k} N={dom.n} G={dom.group} (split-K kernel)"
+    roof["kernel"] = f"ternary GEMM {dom.name}: M={dom.m} K={dom.k} N={dom.n} G={dom.group} (small-token kernel)"
     roof["traffic"] = traffic_of(dom)
 
     details = {"per_gemm_us": {g.name: round(per[g.name] * 1e6, 2) for g in gemms}}

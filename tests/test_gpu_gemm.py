@@ -460,3 +460,48 @@ def test_stream_groups_kernel_every_output(dev, orc, m, k, n_out, grid):
                 os.environ.pop(v, None)
             else:
                 os.environ[v] = val
+
+
+@pytest.mark.parametrize("tile,group,m,k", [
+    ("1x8", 0, 100, 1024), ("2x4", 0, 100, 256), ("2x8", 0, 53, 4096), ("3x2", 0, 100, 4096),
+    ("3x4", 0, 338, 512), ("3x8", 0, 100, 1024), ("1x8", 0, 70, 2048), ("2x8", 0, 100, 2048),
+    ("1x8", 128, 100, 1024), ("2x4", 128, 53, 512), ("2x8", 128, 100, 4096), ("3x2", 128, 100, 4096),
+    ("3x4", 128, 338, 1024), ("3x8", 128, 100, 1024), ("1x8", 128, 70, 2048), ("2x4", 128, 100, 1024)])
+def test_small_kernel_every_output(dev, orc, tile, group, m, k):
+    """The small-token kernel (one round of workgroups, K split over the four wavefronts, int32 partial sums
+    reduced in LDS), forced with each of its tiles on ragged token counts: one group (G = K, K = 256 .. 4096, ring
+    depths 1 .. 8) and 128-column groups (the model format, 4 .. 32 groups folded chunk by chunk); each epilogue
+    with and without bias, every output bit-exact."""
+    import voxrt_amd as vx
+
+    n_out = 256
+    g = k if group == 0 else group
+    trits, s16, x = _workload(orc, m, k, n_out, g, seed_cfg=7)
+    ws = orc.f16_to_f32(s16)
+    if group == 0:
+        w = vx.TernaryMatrix.from_packed_f32(synth.pack_rows(trits), ws, n_out, k, k)
+    else:
+        w = vx.TernaryMatrix.from_packed(synth.pack_rows(trits), s16, n_out, k, group)
+    q, xs, _ = orc.quantize(x, g)
+    xa = vx.QuantAct.quantize(_t(x, dev), g)
+    rng = synth.Lcg(47)
+    base = ((rng.take(m * n_out) % 200).astype(np.float32) * np.float32(0.01) - np.float32(1.0)).reshape(m, n_out)
+    bias = (rng.take(n_out) % 100).astype(np.float32) / np.float32(10.0)
+    old = {v: os.environ.get(v) for v in ("VX_GEMM", "VX_SMALL_TILE")}
+    os.environ["VX_GEMM"] = "small"
+    os.environ["VX_SMALL_TILE"] = tile
+    try:
+        for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
+            want = orc.gemm(trits, ws, q, xs, g, y=base.copy(), ep=ep_kind, alpha=alpha)
+            for with_bias in (False, True):
+                y = _t(base, dev)
+                vx.gemm_ep(w, xa, y, _t(bias, dev) if with_bias else None, _ep_of(vx, ep_kind, alpha))
+                exp = (want + bias[None, :]).astype(np.float32) if with_bias else want
+                _assert_bits_equal(y.cpu().numpy(), exp, f"small tile={tile} G={g} {m}x{k}x{n_out} ep={ep_kind} "
+                                                         f"bias={with_bias}")
+    finally:
+        for v, val in old.items():
+            if val is None:
+                os.environ.pop(v, None)
+            else:
+                os.environ[v] = val

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libvoxrt_hip.so")
-SOURCES = ["vx_abi.hip", "vx_weights.hip", "vx_quant.hip", "vx_gemm.hip", "vx_gemm_stream.hip", "vx_gemm_stream_g.hip", "vx_glue.hip", "vx_attn.hip",
+SOURCES = ["vx_abi.hip", "vx_weights.hip", "vx_quant.hip", "vx_gemm.hip", "vx_gemm_stream.hip", "vx_gemm_stream_g.hip", "vx_gemm_small.hip", "vx_glue.hip", "vx_attn.hip",
            "vx_encoder.hip"]
 
 HIPCC_FLAGS = [

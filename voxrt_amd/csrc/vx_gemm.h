@@ -1,5 +1,5 @@
 // vx_gemm.h — GEMM launch arguments and operand helpers shared by the GEMM kernels (vx_gemm.hip,
-// vx_gemm_stream.hip).
+// vx_gemm_stream.hip, vx_gemm_stream_g.hip, vx_gemm_small.hip).
 #pragma once
 
 #include <type_traits>
@@ -66,5 +66,9 @@ __device__ __forceinline__ void static_for(F &&f) {
 bool gemm_stream(const GemmArgs &a, int tokens_full, hipStream_t st);
 bool gemm_stream_groups(const GemmArgs &a, int tokens_full, hipStream_t st);
 int cu_count();  // compute units of the current device
+
+// The small-token kernel (vx_gemm_small.hip): one or two rounds of workgroups for a whole-width ternary GEMM of a
+// few hundred tokens. Returns false and launches nothing when the shape or window does not fit it.
+bool gemm_small(const GemmArgs &a, hipStream_t st);
 
 }  // namespace vx

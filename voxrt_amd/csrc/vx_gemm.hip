@@ -1303,6 +1303,7 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
     }
     a.vec_ok = (w->out % 4 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
                (!bias || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
+    if (tern && !g && gemm_small(a, st)) return;
     const Plan p = plan_for(a, tern, g, single);
     if (p.kind == kBig) {
         const dim3 grid((unsigned)((a.r1 - a.n_base + 255) / 256), (unsigned)((a.t1 - a.m_base + 127) / 128));

@@ -1,0 +1,382 @@
+// vx_gemm_small.hip — small-token ternary x int8 GEMM (a few hundred tokens: one utterance's frames) on gfx950 i8
+// MFMA, bit-exact to voxrt's scalar kernel (crates/voxrt/src/kernels/mod.rs:166-210):
+//
+//   acc = 0; for each group g ascending: acc = fma((float)S_g, xs[t][g] * ws[o][g], acc); y = ep(acc) (+ bias)
+//
+// At a few hundred tokens the work of one GEMM is a few microseconds of the whole chip, so the kernel is built for
+// latency: all workgroups of the grid are resident at once (several small ones per CU, which hide each other's
+// memory latency), every workgroup issues all of its loads up front (the K steps of its four wavefronts in a
+// register ring, the scales, the bias and, for AddScaled, the old outputs), and nothing between the first load and
+// the last store waits for memory twice.
+//
+// A workgroup owns a (16 * MT) token x (16 * NT) output-row tile; its four wavefronts split K:
+//   * one group (G = K): wavefront w takes K steps [w * nk / 4, (w + 1) * nk / 4);
+//   * 128-column groups: chunk c holds groups 4c .. 4c + 3 and wavefront w takes group 4c + w (two steps).
+// Operands of v_mfma_i32_16x16x64_i8: A = weight codes (trit + 1) widened to int8 (rows = output rows), B = activations
+// (columns = tokens), both over K columns 16 * (l / 16) .. + 15 of the step for lane l. D element e of lane l is
+// output row 4 * (l / 16) + e of token l % 16, so a lane's four sums of a block leave with one 16-byte LDS write.
+// The int32 sums of the four wavefronts meet in LDS (exact in any order); then each thread owns 8 consecutive
+// output rows of (16 * MT * NT / 32) tokens: for one group it adds the four partial sums and folds once; with
+// groups it folds the chunk's four group sums in ascending group order after every chunk.
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+
+#include "vx_gemm.h"
+
+namespace vx {
+namespace {
+
+constexpr int kMaxG = 32;  // groups staged in LDS (K <= 4096 with 128-column groups)
+
+// MT x NT blocks of 16 x 16; GROUPED: 128-column groups (else one group); D: K steps per wavefront in flight.
+template <int MT, int NT, bool GROUPED, int D, int EP, bool BIAS>
+__global__ __launch_bounds__(256, 1) void tgemm_small_kernel(const GemmArgs a, const int n_mt, const int per_xcd,
+                                                             const int ntiles) {
+    constexpr int BM = 16 * MT, BN = 16 * NT, BNP = BN + 4;  // BNP: LDS row pitch (16-byte shift per token row)
+    constexpr int TPR = BN / 8;                               // fold threads per token row
+    constexpr int RPP = 256 / TPR;                            // token rows per fold pass
+    constexpr int R = (BM + RPP - 1) / RPP;                   // fold passes (the last one partial if BM % RPP)
+    constexpr int QX = GROUPED ? kMaxG * BM / 256 : 1, QW = GROUPED ? kMaxG * BN / 256 : 1;
+    __shared__ __attribute__((aligned(16))) int red[4][BM * BNP];
+    __shared__ __attribute__((aligned(16))) float sxs[GROUPED ? kMaxG * BM : 1], sws[GROUPED ? kMaxG * BN : 1];
+    __shared__ __attribute__((aligned(16))) int sgs[GROUPED ? kMaxG * BM : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, lq = lane >> 4;
+    // workgroup b runs on XCD b % 8; the tiles of one XCD are a contiguous range of the tile order, in which
+    // consecutive tiles share output rows (the weight tile) and walk the token tiles
+    const int b = (int)blockIdx.x, tile = (b & 7) * per_xcd + (b >> 3);
+    if (tile >= ntiles) return;  // the grid is a multiple of 8
+    const int tm = tile % n_mt, tn = tile / n_mt;
+    const int m0 = (int)a.m_base + tm * BM, n0 = tn * BN;
+    const int inp = (int)a.inp, nk = inp / 64, nsteps = nk / 4, ng = (int)a.ng, np = (int)a.np;
+
+    const auto xrs = make_rsrc(a.xq, a.xq_bytes);
+    const auto wrs = make_rsrc(a.w, a.w_bytes);
+    const auto srs = make_rsrc(a.xs, a.xs_bytes);
+    const auto grs = make_rsrc(a.xg, a.xs_bytes);
+    const auto wsrs = make_rsrc(a.ws_t, a.ws_bytes);
+    const auto yrs = make_rsrc(a.y, a.y_bytes);
+    const auto brs = make_rsrc(a.bias, BIAS ? (uint32_t)(a.out * 4) : 0u);
+
+    // fold ownership: token rows tt0 + r * RPP of the tile, output rows c0 .. c0 + 7
+    const int tt0 = tid / TPR, c0 = (tid % TPR) * 8, o0 = n0 + c0;
+    const uint32_t out4 = (uint32_t)a.out * 4;
+
+    // loads that only the fold and the epilogue need, issued before the K loop
+    float xsr[GROUPED ? 1 : R];
+    int gsr[GROUPED ? 1 : R];
+    v4i wlo = v4i{0, 0, 0, 0}, whi = v4i{0, 0, 0, 0};
+    if constexpr (!GROUPED) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            xsr[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, (uint32_t)(m0 + tt0 + r * RPP) * 4, 0, 0));
+            gsr[r] = (int)__builtin_amdgcn_raw_buffer_load_b32(grs, (uint32_t)(m0 + tt0 + r * RPP) * 4, 0, 0);
+        }
+        wlo = __builtin_amdgcn_raw_buffer_load_b128(wsrs, (uint32_t)o0 * 4, 0, 0);
+        whi = __builtin_amdgcn_raw_buffer_load_b128(wsrs, (uint32_t)o0 * 4 + 16, 0, 0);
+    }
+    v4i blo = v4i{0, 0, 0, 0}, bhi = v4i{0, 0, 0, 0};
+    if constexpr (BIAS) {
+        blo = __builtin_amdgcn_raw_buffer_load_b128(brs, (uint32_t)o0 * 4, 0, 0);
+        bhi = __builtin_amdgcn_raw_buffer_load_b128(brs, (uint32_t)o0 * 4 + 16, 0, 0);
+    }
+    v4i olo[EP == VX_EP_ADD_SCALED ? R : 1], ohi[EP == VX_EP_ADD_SCALED ? R : 1];
+    if constexpr (EP == VX_EP_ADD_SCALED) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t so = (uint32_t)(m0 + tt0 + r * RPP) * out4 + (uint32_t)o0 * 4;
+            olo[r] = __builtin_amdgcn_raw_buffer_load_b128(yrs, so, 0, 0);
+            ohi[r] = __builtin_amdgcn_raw_buffer_load_b128(yrs, so + 16, 0, 0);
+        }
+    }
+    // groups: the token scales, code sums and weight scales of every group of the tile, loaded here and written to
+    // LDS at the first chunk's fold (entries past the last group read zeros and are never used)
+    uint32_t qx[QX], qg[QX], qw[QW];
+    if constexpr (GROUPED) {
+#pragma unroll
+        for (int q = 0; q < QX; q++) {
+            const int i = tid + 256 * q, g = i / BM, k = i % BM;
+            const uint32_t off = g < ng ? (uint32_t)(g * np + m0 + k) * 4 : kOff;
+            qx[q] = __builtin_amdgcn_raw_buffer_load_b32(srs, off, 0, 0);
+            qg[q] = __builtin_amdgcn_raw_buffer_load_b32(grs, off, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < QW; q++) {
+            const int i = tid + 256 * q, g = i / BN, k = i % BN;
+            qw[q] = __builtin_amdgcn_raw_buffer_load_b32(wsrs, g < ng ? (uint32_t)(g * (int)a.out_pad + n0 + k) * 4 : kOff,
+                                                         0, 0);
+        }
+    }
+
+    // the K loop: step i of this wavefront is global step kb_of(i); activations of token m0 + 16 mb + l16 (a token
+    // past n reads zeros: its offset lies past the end of xq), weight codes one dword per lane and block
+    uint32_t va[MT];
+#pragma unroll
+    for (int mb = 0; mb < MT; mb++) va[mb] = (uint32_t)(m0 + 16 * mb + l16) * (uint32_t)inp + 16 * lq;
+    auto kb_of = [&](int i) __attribute__((always_inline)) {
+        return GROUPED ? ((i >> 1) * 4 + wave) * 2 + (i & 1) : wave * nsteps + i;
+    };
+    v4i ra[D][MT];
+    uint32_t rb[D][NT];
+    auto issue = [&](int i, int slot) __attribute__((always_inline)) {
+        const int kb = kb_of(i);
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++) ra[slot][mb] = __builtin_amdgcn_raw_buffer_load_b128(xrs, va[mb], kb * 64, 0);
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++)
+            rb[slot][nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)lane * 4, ((n0 / 16 + nb) * nk + kb) * 256, 0);
+    };
+
+    // the weight operand is the code trit + 1, so a group's sum over its columns is S_g + sum(x codes) of the token
+    // and group, and the fold subtracts the quantizer's gsum (exact in int32)
+    v4i acc[MT][NT];
+#pragma unroll
+    for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++) acc[mb][nb] = v4i{0, 0, 0, 0};
+    float accf[R][8];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) accf[r][j] = 0.0f;
+
+    // int32 sums of this wavefront -> its LDS plane (one 16-byte write per block)
+    auto to_lds = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++)
+                *(v4i *)&red[wave][(16 * mb + l16) * BNP + 16 * nb + 4 * lq] = acc[mb][nb];
+    };
+
+    // step i of this wavefront from ring slot `slot`; with groups D is even, so the step's position in its group
+    // is the slot's parity (known at compile time)
+    auto compute = [&](int slot, int i) __attribute__((always_inline)) {
+        v4i bw[NT];
+#pragma unroll
+        for (int nb = 0; nb < NT; nb++) bw[nb] = widen_codes(rb[slot][nb]);
+        const bool first = GROUPED && (slot & 1) == 0;  // a group's chain starts from zero
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++)
+                acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[nb], ra[slot][mb],
+                                                                     first ? v4i{0, 0, 0, 0} : acc[mb][nb], 0, 0, 0);
+        if constexpr (GROUPED) {
+            if ((slot & 1) == 1) {  // chunk (i >> 1) complete: fold groups 4c .. 4c + 3 in ascending order
+                if (i == 1) {
+#pragma unroll
+                    for (int q = 0; q < QX; q++)
+                        if (tid + 256 * q < kMaxG * BM) {
+                            sxs[tid + 256 * q] = __uint_as_float(qx[q]);
+                            sgs[tid + 256 * q] = (int)qg[q];
+                        }
+#pragma unroll
+                    for (int q = 0; q < QW; q++)
+                        if (tid + 256 * q < kMaxG * BN) sws[tid + 256 * q] = __uint_as_float(qw[q]);
+                }
+                to_lds();
+                __syncthreads();
+                const int c = i >> 1;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const int g = 4 * c + w;
+                    const float4 wa = *(const float4 *)&sws[g * BN + c0];
+                    const float4 wb = *(const float4 *)&sws[g * BN + c0 + 4];
+                    const float wsv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        const int tt = tt0 + r * RPP;
+                        if (BM % RPP != 0 && tt >= BM) continue;
+                        const float xs = sxs[g * BM + tt];
+                        const int gsum = sgs[g * BM + tt];
+                        const v4i lo = *(const v4i *)&red[w][tt * BNP + c0];
+                        const v4i hi = *(const v4i *)&red[w][tt * BNP + c0 + 4];
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            accf[r][j] = __builtin_fmaf((float)(lo[j] - gsum), xs * wsv[j], accf[r][j]);
+                            accf[r][4 + j] = __builtin_fmaf((float)(hi[j] - gsum), xs * wsv[4 + j], accf[r][4 + j]);
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+    };
+
+    // nsteps is a multiple of D (the host picks D): prologue, steady state, drain
+#pragma unroll
+    for (int i = 0; i < D; i++) issue(i, i);
+    for (int s0 = 0; s0 < nsteps - D; s0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; i++) {
+            compute(i, s0 + i);
+            issue(s0 + i + D, i);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < D; i++) compute(i, nsteps - D + i);
+
+    if constexpr (!GROUPED) {
+        to_lds();
+        __syncthreads();
+        const float wsv[8] = {__int_as_float(wlo[0]), __int_as_float(wlo[1]), __int_as_float(wlo[2]),
+                              __int_as_float(wlo[3]), __int_as_float(whi[0]), __int_as_float(whi[1]),
+                              __int_as_float(whi[2]), __int_as_float(whi[3])};
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int tt = tt0 + r * RPP;
+            if (BM % RPP != 0 && tt >= BM) continue;
+            int S[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) S[j] = -gsr[r];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const v4i lo = *(const v4i *)&red[w][tt * BNP + c0];
+                const v4i hi = *(const v4i *)&red[w][tt * BNP + c0 + 4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    S[j] += lo[j];
+                    S[4 + j] += hi[j];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) accf[r][j] = __builtin_fmaf((float)S[j], xsr[r] * wsv[j], 0.0f);
+        }
+    }
+
+    // epilogue (kernels/mod.rs:41-48), bias after it; tokens outside [t0, t1) are not written
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int t = m0 + tt0 + r * RPP;
+        v4i lo, hi;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float v = accf[r][j];
+            float res = v;
+            if constexpr (EP == VX_EP_SILU) res = silu_fast(v);
+            if constexpr (EP == VX_EP_ADD_SCALED)
+                res = __builtin_fmaf(a.alpha, v, __int_as_float(j < 4 ? olo[r][j] : ohi[r][j - 4]));
+            if constexpr (BIAS) res = res + __int_as_float(j < 4 ? blo[j] : bhi[j - 4]);
+            if (j < 4)
+                lo[j] = __float_as_int(res);
+            else
+                hi[j - 4] = __float_as_int(res);
+        }
+        if (t >= a.t0 && t < a.t1 && (BM % RPP == 0 || tt0 + r * RPP < BM)) {
+            const uint32_t so = (uint32_t)t * out4 + (uint32_t)o0 * 4;
+            __builtin_amdgcn_raw_buffer_store_b128(lo, yrs, so, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(hi, yrs, so + 16, 0, 0);
+        }
+    }
+}
+
+// deepest ring of K steps whose operands (MT activation and NT weight registers per step) fit in 128 registers
+constexpr int max_ring(int mt, int nt) { return 128 / (4 * mt + nt) >= 8 ? 8 : 128 / (4 * mt + nt) >= 4 ? 4 : 2; }
+
+struct SmallPlan {
+    int mt = 0, nt = 0, d = 0, tiles = 0;
+};
+
+bool tile_ok(const GemmArgs &a, int mt, int nt) {
+    static const int tiles[][2] = {{1, 8}, {2, 4}, {2, 8}, {3, 2}, {3, 4}, {3, 8}};
+    for (const auto &t : tiles)
+        if (t[0] == mt && t[1] == nt) return a.out % (16 * nt) == 0;
+    return false;
+}
+
+// Tile choice, from measurements of the encoder's shapes at 125, 338 and 750 tokens: with one group, 16 x 128 tiles
+// (several small workgroups per CU hide each other's memory latency); with 128-column
+// groups 32 x 64 tiles below 512 tokens, except for the wide projections from K = 1024 (N >= 3072: q|k|v, FFN up) at
+// 256 tokens or more, where the split-K kernel over groups is as fast or faster.
+SmallPlan plan_small(const GemmArgs &a, bool grouped, int force_mt, int force_nt) {
+    const int64_t ntok = a.t1 - a.m_base, nk = a.inp / 64;
+    SmallPlan best;
+    if (force_mt) {
+        if (tile_ok(a, force_mt, force_nt)) best.mt = force_mt, best.nt = force_nt;
+    } else if (!grouped) {
+        if (tile_ok(a, 1, 8))
+            best.mt = 1, best.nt = 8;
+        else if (tile_ok(a, 2, 4))
+            best.mt = 2, best.nt = 4;
+        else if (tile_ok(a, 3, 2))
+            best.mt = 3, best.nt = 2;
+    } else if (ntok < 512 && !(a.inp <= 1024 && a.out >= 3072 && ntok >= 256)) {
+        if (tile_ok(a, 2, 4))
+            best.mt = 2, best.nt = 4;
+        else if (tile_ok(a, 3, 2))
+            best.mt = 3, best.nt = 2;
+    }
+    if (best.mt) best.tiles = (int)((ntok + 16 * best.mt - 1) / (16 * best.mt) * (a.out / (16 * best.nt)));
+    if (best.mt == 0) return best;
+    // ring depth: a power of two dividing the wavefront's steps, at most 128 registers of operands in flight
+    const int steps = (int)(nk / 4), dmax = max_ring(best.mt, best.nt);
+    best.d = 1;
+    while (best.d * 2 <= dmax && steps % (best.d * 2) == 0) best.d *= 2;
+    if (grouped && best.d < 2) best.mt = 0;  // a group is two steps
+    return best;
+}
+
+template <int MT, int NT, bool GROUPED, int D>
+void launch_small_ep(const GemmArgs &a, int grid, int n_mt, int per_xcd, int ntiles, hipStream_t st) {
+    const bool bias = a.bias != nullptr;
+#define VX_SMALL(EP)                                                                                              \
+    (bias ? tgemm_small_kernel<MT, NT, GROUPED, D, EP, true> : tgemm_small_kernel<MT, NT, GROUPED, D, EP, false>)
+    auto k = a.ep == VX_EP_SILU ? VX_SMALL(VX_EP_SILU) : a.ep == VX_EP_ADD_SCALED ? VX_SMALL(VX_EP_ADD_SCALED)
+                                                                                  : VX_SMALL(VX_EP_STORE);
+#undef VX_SMALL
+    k<<<grid, 256, 0, st>>>(a, n_mt, per_xcd, ntiles);
+}
+
+template <int MT, int NT, bool GROUPED>
+void launch_small_d(const GemmArgs &a, int d, int grid, int n_mt, int per_xcd, int ntiles, hipStream_t st) {
+    if constexpr (max_ring(MT, NT) >= 8)
+        if (d == 8) return launch_small_ep<MT, NT, GROUPED, 8>(a, grid, n_mt, per_xcd, ntiles, st);
+    if (d == 4)
+        launch_small_ep<MT, NT, GROUPED, 4>(a, grid, n_mt, per_xcd, ntiles, st);
+    else if (d == 2)
+        launch_small_ep<MT, NT, GROUPED, 2>(a, grid, n_mt, per_xcd, ntiles, st);
+    else if constexpr (!GROUPED)
+        launch_small_ep<MT, NT, GROUPED, 1>(a, grid, n_mt, per_xcd, ntiles, st);
+}
+
+template <bool GROUPED>
+void launch_small(const GemmArgs &a, const SmallPlan &p, int grid, int n_mt, int per_xcd, int ntiles, hipStream_t st) {
+#define VX_TILE(M, N)                                                                                             \
+    if (p.mt == M && p.nt == N) return launch_small_d<M, N, GROUPED>(a, p.d, grid, n_mt, per_xcd, ntiles, st);
+    VX_TILE(1, 8) VX_TILE(2, 4) VX_TILE(2, 8) VX_TILE(3, 2) VX_TILE(3, 4) VX_TILE(3, 8)
+#undef VX_TILE
+}
+
+}  // namespace
+
+bool gemm_small(const GemmArgs &a, hipStream_t st) {
+    const bool grouped = a.ng > 1;
+    if (a.gs != nullptr || a.y_bytes == 0 || !a.vec_ok) return false;
+    if (a.r0 != 0 || a.r1 != a.out || a.n_base != 0) return false;
+    if (grouped ? (a.spg != 2 || a.ng % 4 != 0 || a.ng > kMaxG) : (a.inp / 64) % 4 != 0) return false;
+    // VX_GEMM=small forces this kernel (=stream keeps it for the tokens after the streaming kernel's tiles; any
+    // other value turns it off); VX_SMALL_TILE=MTxNT forces a tile (tests and tuning)
+    const char *kv = getenv("VX_GEMM");
+    if (kv && *kv && strcmp(kv, "small") != 0 && strcmp(kv, "stream") != 0) return false;
+    int fm = 0, fn = 0;
+    const char *tv = getenv("VX_SMALL_TILE");
+    if (tv && *tv && sscanf(tv, "%dx%d", &fm, &fn) != 2) fm = fn = 0;
+    // up to 1024 tokens; longer token ranges go to the kernels built for throughput
+    if (a.t1 - a.m_base > 1024 && !(kv && strcmp(kv, "small") == 0)) return false;
+    const SmallPlan p = plan_small(a, grouped, fm, fn);
+    if (p.mt == 0) return false;
+    const int64_t ntok = a.t1 - a.m_base;
+    const int n_mt = (int)((ntok + 16 * p.mt - 1) / (16 * p.mt));
+    const int per_xcd = (p.tiles + 7) / 8;  // grid 8 * per_xcd; workgroups past the last tile return at once
+    if (grouped)
+        launch_small<true>(a, p, 8 * per_xcd, n_mt, per_xcd, p.tiles, st);
+    else
+        launch_small<false>(a, p, 8 * per_xcd, n_mt, per_xcd, p.tiles, st);
+    hip_check(hipGetLastError(), "tgemm_small launch");
+    return true;
+}
+
+}  // namespace vx
