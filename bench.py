@@ -330,6 +330,8 @@ def main():
     ap.add_argument("--no-encoder", action="store_true", help="skip the 24-layer encoder RTFx leg")
     ap.add_argument("--encoder-only", action="store_true",
                     help="only the 24-layer encoder RTFx leg (prints its JSON and exits)")
+    ap.add_argument("--gemm", type=int, nargs=4, metavar=("M", "K", "N", "G"),
+                    help="run only this GEMM (Store epilogue), 6 eager launches: for counter collection")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (the counter calibration of the traffic figure)")
     args = ap.parse_args()
@@ -355,6 +357,14 @@ def main():
 
     vx.kernels.check(vx.lib().vx_init(0))
     dev = torch.device("cuda:0")
+    if args.gemm:
+        m, k, n, grp = args.gemm
+        g = Gemm(vx, synth, dev, "gemm", m, k, n, 0, 0.0, grp, 2, 1)
+        for _ in range(6):
+            g.run()
+        torch.cuda.synchronize()
+        print(json.dumps({"gemm": f"{m}x{k}x{n}:G{grp}", "launches": 6, "ops_per_launch": g.ops}), flush=True)
+        return
     if args.encoder_only:
         enc, eparams, esp = encoder_setup(synth)
         out = {"encoder": encoder_rtfx(torch, synth, enc, dev)}
