@@ -10,6 +10,7 @@
  *   vx_tmat_free / vx_tmat_info       <- drop / the out, inp, group, ternary fields (packed.rs:48-60)
  *   vx_quantize                       <- QuantAct::quantize_layout (packed.rs:307-436, quantize_group 527-535)
  *   vx_gemm_ep                        <- kernels::gemm_ep / gemm (kernels/mod.rs:319-362)
+ *   vx_gemm_ep_quantize               <- FeedForward::forward_fused's up-projection + prepare (encoder.rs:87-89)
  *   vx_gemm_rows_range                <- kernels::gemm_rows_range (kernels/mod.rs:257-282)
  *   vx_gemm_single                    <- kernels::gemm_single (kernels/mod.rs:285-316)
  *   vx_quantize_normed                <- TernaryLinear::prepare_normed (ternary_linear.rs:132-155)
@@ -99,6 +100,17 @@ vx_status vx_quantize(const float *x, int64_t n, int64_t inp, int64_t group, int
  * group_sums[(g*n + t)*out + o] (int32 [inp/group, n, out]). */
 vx_status vx_gemm_ep(const vx_tmat *w, const int8_t *xq, const float *xs_t, const int32_t *xgsum_t, int64_t n,
                      float *y, const float *bias, int ep, float alpha, int32_t *group_sums, void *stream);
+
+/* gemm_ep + prepare fused: the FFN up-projection followed by the down-projection's activation quantization
+ * (FeedForward::forward_fused, encoder.rs:87-89: w1.forward_prepared_ep(a, t, hbuf, Epilogue::Silu), then
+ * w2.prepare(hbuf, t) = QuantAct::quantize_layout, packed.rs:307-436). y = ep(x . w^T) (+ bias) with ep Store or
+ * Silu, quantized in `group`-column groups into q int8 [n, out], scales_t float32 and gsum_t int32
+ * [out/group, VX_NPAD(n)] (pad tokens zero), bit for bit as vx_gemm_ep followed by vx_quantize. y_tmp float32
+ * [n, out] is scratch: with 128-column groups and n <= 1024 the GEMM quantizes in its epilogue and y_tmp is not
+ * touched (it may then be NULL); other shapes write y there and quantize it. */
+vx_status vx_gemm_ep_quantize(const vx_tmat *w, const int8_t *xq, const float *xs_t, const int32_t *xgsum_t,
+                              int64_t n, float *y_tmp, const float *bias, int ep, int64_t group, int8_t *q,
+                              float *scales_t, int32_t *gsum_t, void *stream);
 
 /* gemm_rows_range: as vx_gemm_ep without bias, writing only rows o in [r0, r1) and tokens t in [t0, t1) of
  * y [n, out]; nothing else in y is read or written. */

@@ -505,3 +505,41 @@ def test_small_kernel_every_output(dev, orc, tile, group, m, k):
                 os.environ.pop(v, None)
             else:
                 os.environ[v] = val
+
+
+@pytest.mark.parametrize("m,k,n_out,group,ep_kind,with_bias", [
+    (338, 1024, 4096, 128, 1, False),   # the encoder's FFN up-projection at T = 338 (fused epilogue)
+    (338, 1024, 4096, 0, 1, True),      # one group (G = K), bias after SiLU
+    (70, 1024, 384, 128, 0, True),      # ragged tokens, three output groups, Store
+    (125, 4096, 256, 128, 1, False),    # 32 input groups (ring depth 8)
+    (1100, 1024, 512, 128, 1, True)])   # above 1024 tokens: GEMM into y_tmp, then the quantizer
+def test_gemm_ep_quantize_equals_two_step(dev, orc, m, k, n_out, group, ep_kind, with_bias):
+    """gemm_ep_quantize (the FFN up-projection with the down-projection's quantization fused) equals the reference
+    chain forward_prepared_ep(Silu) -> QuantAct::quantize_layout of the oracle: int8 codes, scales and code sums
+    bit for bit, pad tokens of the transposed scales and sums zero."""
+    import torch
+
+    import voxrt_amd as vx
+
+    g = k if group == 0 else group
+    trits, s16, x = _workload(orc, m, k, n_out, g, seed_cfg=8)
+    ws = orc.f16_to_f32(s16)
+    if group == 0:
+        w = vx.TernaryMatrix.from_packed_f32(synth.pack_rows(trits), ws, n_out, k, k)
+    else:
+        w = vx.TernaryMatrix.from_packed(synth.pack_rows(trits), s16, n_out, k, group)
+    q, xs, _ = orc.quantize(x, g)
+    xa = vx.QuantAct.quantize(_t(x, dev), g)
+    bias = (synth.Lcg(53).take(n_out) % 100).astype(np.float32) / np.float32(10.0) - np.float32(5.0)
+    want = orc.gemm(trits, ws, q, xs, g, ep=ep_kind)
+    if with_bias:
+        want = (want + bias[None, :]).astype(np.float32)
+    wq, wsc, wgs = orc.quantize(want, 128)
+    got = vx.gemm_ep_quantize(w, xa, _t(bias, dev) if with_bias else None, _ep_of(vx, ep_kind, 0.0), 128)
+    torch.cuda.synchronize()
+    tag = f"{m}x{k}x{n_out} G={g} ep={ep_kind} bias={with_bias}"
+    np.testing.assert_array_equal(got.x.cpu().numpy(), wq, err_msg=f"codes {tag}")
+    st, gt = got.scales_t.cpu().numpy(), got.gsum_t.cpu().numpy()
+    _assert_bits_equal(st[:, :m].T.copy(), wsc, f"scales {tag}")
+    np.testing.assert_array_equal(gt[:, :m].T, wgs, err_msg=f"gsum {tag}")
+    assert not st[:, m:].any() and not gt[:, m:].any(), f"pad tokens not zero {tag}"

@@ -19,6 +19,8 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
           hipStream_t st);
 void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const float *g, const float *b, int8_t *q,
                  float *scales_t, int32_t *gsum_t, hipStream_t stream);
+void gemm_quant(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y_tmp,
+                const float *bias, int ep, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st);
 void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y, hipStream_t stream);
 void glu_dwconv_silu(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t, const float *bias, float *out,
                      hipStream_t st);
@@ -160,6 +162,16 @@ vx_status vx_gemm_ep(const vx_tmat *w, const int8_t *xq, const float *xs_t, cons
         vx::require(w != nullptr, "weight matrix must not be NULL");
         const vx::TMat *m = unwrap(w);
         vx::gemm(m, xq, xs_t, xgsum_t, n, y, bias, ep, alpha, group_sums, 0, m->out, 0, n, (hipStream_t)stream);
+    });
+}
+
+vx_status vx_gemm_ep_quantize(const vx_tmat *w, const int8_t *xq, const float *xs_t, const int32_t *xgsum_t,
+                              int64_t n, float *y_tmp, const float *bias, int ep, int64_t group, int8_t *q,
+                              float *scales_t, int32_t *gsum_t, void *stream) {
+    return guarded([&] {
+        vx::require(w != nullptr, "weight matrix must not be NULL");
+        vx::gemm_quant(unwrap(w), xq, xs_t, xgsum_t, n, y_tmp, bias, ep, group, q, scales_t, gsum_t,
+                       (hipStream_t)stream);
     });
 }
 

@@ -9,7 +9,7 @@
 // Forward for t frames (a workspace per distinct t is kept; the relative position table of t is computed on the
 // host once, uploaded and quantized once, since every layer's relative_k_proj consumes the same table):
 //   per layer, in place on the residual stream x [t][d] (ConformerLayer::forward_profiled, encoder.rs:706-756):
-//     ff1:  q = LNquant(x); h = silu(W1 q); x = fma(0.5, W2 quant(h), x)
+//     ff1:  q = LNquant(x); h = silu(W1 q); x = fma(0.5, W2 quant(h), x)   (W1's GEMM writes quant(h) itself)
 //     attn: q = LNquant(x); qkv = Wqkv q; rel = Wpos quant(pos); ctx = core(qkv, rel); x = fma(1, Wo quant(ctx), x)
 //     conv: q = LNquant(x); g = Wpw1 q; hb = silu(dwconv_bn(glu(g))); x = fma(1, Wpw2 quant(hb), x)
 //     ff2 as ff1; x' = LN_out(x) into the other half of a ping-pong pair.
@@ -32,6 +32,8 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
           hipStream_t st);
 void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const float *g, const float *b, int8_t *q,
                  float *scales_t, int32_t *gsum_t, hipStream_t stream);
+void gemm_quant(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y_tmp,
+                const float *bias, int ep, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st);
 void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y, hipStream_t stream);
 void glu_dwconv_silu_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
                          const float *bias, float *out, hipStream_t st);
@@ -204,8 +206,10 @@ void run_layers(vx_encoder *e, EncWs &w, hipStream_t st) {
         };
         auto ffn = [&](int norm, int w1, int w2) {
             lnq(norm);
-            gemm_full(L.lin[w1], w.a, t, w.hbuf.as<float>(), VX_EP_SILU, 0.0f, st);
-            quant(w.hbuf.as<float>(), c.ff, w.f);
+            // h = silu(W1 q) quantized for W2 in one call (up to 1024 rows the GEMM quantizes in its epilogue and
+            // h never reaches memory; above, hbuf carries it)
+            gemm_quant(&L.lin[w1]->m, w.a.q.as<int8_t>(), w.a.s.as<float>(), w.a.g.as<int32_t>(), t, w.hbuf.as<float>(),
+                       nullptr, VX_EP_SILU, G, w.f.q.as<int8_t>(), w.f.s.as<float>(), w.f.g.as<int32_t>(), st);
             gemm_full(L.lin[w2], w.f, t, x, VX_EP_ADD_SCALED, 0.5f, st);
         };
         ffn(0, 0, 1);

@@ -23,6 +23,11 @@ struct GemmArgs {
     int ep;
     float alpha;
     int vec_ok;  // y (and bias) rows are 16-byte aligned: out % 4 == 0 and 16-byte aligned base pointers
+    // quantized output (the next GEMM's activations, 128-column groups): codes [n][out], scales_t and gsum_t
+    // [out/128][np]; NULL qo: y is written
+    int8_t *qo;
+    float *qs;
+    int32_t *qg;
 };
 
 __device__ inline v4i widen_codes(uint32_t p) {

@@ -1246,11 +1246,12 @@ void run_lds(const GemmArgs &a, bool tern, bool gs, bool single, int d, hipStrea
 
 }  // namespace
 
-void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y,
-          const float *bias, int ep, float alpha, int32_t *gs, int64_t r0, int64_t r1, int64_t t0, int64_t t1,
-          hipStream_t st) {
+// Checks the operands of a GEMM call and fills its launch arguments (y may be NULL only for a quantized output).
+static GemmArgs gemm_args(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n,
+                          float *y, const float *bias, int ep, float alpha, int32_t *gs, int64_t r0, int64_t r1,
+                          int64_t t0, int64_t t1, bool y_needed) {
     require(w != nullptr, "weight matrix must not be NULL");
-    require(xq && xs_t && y, "xq, xs_t and y must not be NULL");
+    require(xq && xs_t && (y || !y_needed), "xq, xs_t and y must not be NULL");
     require(!w->ternary || xg_t, "ternary weights need the activation code sums (xgsum_t)");
     require(ep == VX_EP_STORE || ep == VX_EP_SILU || ep == VX_EP_ADD_SCALED, "unknown epilogue");
     require(n >= 0, "n must be >= 0");
@@ -1258,8 +1259,7 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
     require(0 <= t0 && t0 <= t1 && t1 <= n, "token range outside [0, n]");
     const int64_t np = (n + 15) / 16 * 16;
     require((np + 256) * w->inp < (1ll << 31) && np * w->ng * 4 < (1ll << 31), "activation operand above 2 GiB");
-    if (r0 == r1 || t0 == t1) return;
-    GemmArgs a;
+    GemmArgs a{};
     a.w = w->wdev;
     a.ws_t = w->scales_t;
     a.xq = xq;
@@ -1290,6 +1290,16 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
     a.y_bytes = n * w->out * 4 < (1ll << 31) ? (uint32_t)(n * w->out * 4) : 0u;  // 0: no buffer stores
     a.ep = ep;
     a.alpha = alpha;
+    a.vec_ok = (w->out % 4 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
+               (!bias || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
+    return a;
+}
+
+void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y,
+          const float *bias, int ep, float alpha, int32_t *gs, int64_t r0, int64_t r1, int64_t t0, int64_t t1,
+          hipStream_t st) {
+    GemmArgs a = gemm_args(w, xq, xs_t, xg_t, n, y, bias, ep, alpha, gs, r0, r1, t0, t1, true);
+    if (r0 == r1 || t0 == t1) return;
     const bool tern = w->ternary, g = gs != nullptr, single = w->ng == 1;
     // whole 128-token tiles of a full-width ternary GEMM (one group or 128-column groups): the streaming kernels;
     // the remaining tokens (fewer than 128) go through the kernels below
@@ -1301,8 +1311,6 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
             a.m_base = full;
         }
     }
-    a.vec_ok = (w->out % 4 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
-               (!bias || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
     if (tern && !g && gemm_small(a, st)) return;
     const Plan p = plan_for(a, tern, g, single);
     if (p.kind == kBig) {
@@ -1347,6 +1355,32 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
             run_lds<2, 4>(a, tern, g, single, d, st);
     }
     hip_check(hipGetLastError(), "tgemm launch");
+}
+
+void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const float *g, const float *b, int8_t *q,
+                 float *scales_t, int32_t *gsum_t, hipStream_t stream);
+
+// The FFN up-projection with the down-projection's quantization fused (encoder.rs:87-89: forward_prepared_ep with
+// Silu into hbuf, then prepare(hbuf) = QuantAct::quantize_layout, packed.rs:307-436): y = ep(x . w^T) (+ bias),
+// quantized in `group`-column groups into q [n][out], scales_t and gsum_t [out/group][npad(n)]. With 128-column
+// groups and up to 1024 tokens the small-token kernel quantizes in its epilogue and y never reaches memory; other
+// shapes run the GEMM into y_tmp and then the quantizer. The codes equal those of the two-step chain bit for bit.
+void gemm_quant(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y_tmp,
+                const float *bias, int ep, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st) {
+    require(q && scales_t && gsum_t, "q, scales_t and gsum_t must not be NULL");
+    require(ep == VX_EP_STORE || ep == VX_EP_SILU, "a quantized output takes the Store or Silu epilogue");
+    require(w != nullptr && group > 0 && w->out % group == 0, "out must be a positive multiple of group");
+    GemmArgs a = gemm_args(w, xq, xs_t, xg_t, n, y_tmp, bias, ep, 0.0f, nullptr, 0, w->out, 0, n, false);
+    if (n == 0) return;
+    if (w->ternary && group == 128) {
+        a.qo = q;
+        a.qs = scales_t;
+        a.qg = gsum_t;
+        if (gemm_small(a, st)) return;
+    }
+    require(y_tmp != nullptr, "y_tmp must not be NULL for this shape (the GEMM output goes through it)");
+    gemm(w, xq, xs_t, xg_t, n, y_tmp, bias, ep, 0.0f, nullptr, 0, w->out, 0, n, st);
+    quantize_ln(y_tmp, n, w->out, group, nullptr, nullptr, q, scales_t, gsum_t, st);
 }
 
 }  // namespace vx

@@ -18,6 +18,11 @@
 // The int32 sums of the four wavefronts meet in LDS (exact in any order); then each thread owns 8 consecutive
 // output rows of (16 * MT * NT / 32) tokens: for one group it adds the four partial sums and folds once; with
 // groups it folds the chunk's four group sums in ascending group order after every chunk.
+//
+// Quantized output (16 x 128 tiles): instead of y, the epilogue writes the next GEMM's activations. The 16 fold
+// threads of a token hold its 128 outputs of one 128-column group after the epilogue and bias, so the group's
+// quantization (QuantAct::quantize_group, packed.rs:527-535: amax, s = amax / 127 or 1, inv = 1 / s, codes
+// clamp(rint(x * inv)), code sum) reduces over those 16 lanes, and the f32 outputs never reach memory.
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
@@ -30,7 +35,7 @@ namespace {
 constexpr int kMaxG = 32;  // groups staged in LDS (K <= 4096 with 128-column groups)
 
 // MT x NT blocks of 16 x 16; GROUPED: 128-column groups (else one group); D: K steps per wavefront in flight.
-template <int MT, int NT, bool GROUPED, int D, int EP, bool BIAS>
+template <int MT, int NT, bool GROUPED, int D, int EP, bool BIAS, bool QOUT>
 __global__ __launch_bounds__(256, 1) void tgemm_small_kernel(const GemmArgs a, const int n_mt, const int per_xcd,
                                                              const int ntiles) {
     constexpr int BM = 16 * MT, BN = 16 * NT, BNP = BN + 4;  // BNP: LDS row pitch (16-byte shift per token row)
@@ -38,6 +43,8 @@ __global__ __launch_bounds__(256, 1) void tgemm_small_kernel(const GemmArgs a, c
     constexpr int RPP = 256 / TPR;                            // token rows per fold pass
     constexpr int R = (BM + RPP - 1) / RPP;                   // fold passes (the last one partial if BM % RPP)
     constexpr int QX = GROUPED ? kMaxG * BM / 256 : 1, QW = GROUPED ? kMaxG * BN / 256 : 1;
+    static_assert(!QOUT || (BN == 128 && BM % RPP == 0 && EP != VX_EP_ADD_SCALED),
+                  "a quantized output group is one token row of a 128-row tile");
     __shared__ __attribute__((aligned(16))) int red[4][BM * BNP];
     __shared__ __attribute__((aligned(16))) float sxs[GROUPED ? kMaxG * BM : 1], sws[GROUPED ? kMaxG * BN : 1];
     __shared__ __attribute__((aligned(16))) int sgs[GROUPED ? kMaxG * BM : 1];
@@ -265,7 +272,38 @@ __global__ __launch_bounds__(256, 1) void tgemm_small_kernel(const GemmArgs a, c
             else
                 hi[j - 4] = __float_as_int(res);
         }
-        if (t >= a.t0 && t < a.t1 && (BM % RPP == 0 || tt0 + r * RPP < BM)) {
+        if constexpr (QOUT) {
+            // quantize_group over the token's 128 outputs: 8 per lane on 16 adjacent lanes
+            float m = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(__int_as_float(lo[j])), fabsf(__int_as_float(hi[j]))));
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            const float s = m == 0.0f ? 1.0f : m / 127.0f;
+            const float inv = 1.0f / s;
+            uint32_t w0 = 0, w1 = 0;
+            int sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int8_t c0 = code_of(__int_as_float(lo[j]), inv), c1 = code_of(__int_as_float(hi[j]), inv);
+                sum += (int)c0 + (int)c1;
+                w0 |= (uint32_t)(uint8_t)c0 << (8 * j);
+                w1 |= (uint32_t)(uint8_t)c1 << (8 * j);
+            }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            const int64_t gi = (int64_t)(o0 / 128) * a.np + t;
+            if (t < a.n) {
+                *(uint2 *)(a.qo + (int64_t)t * a.out + o0) = make_uint2(w0, w1);
+                if ((tid & 15) == 0) {
+                    a.qs[gi] = s;
+                    a.qg[gi] = sum;
+                }
+            } else if (t < a.np && (tid & 15) == 0) {  // pad tokens: zero scale and code sum
+                a.qs[gi] = 0.0f;
+                a.qg[gi] = 0;
+            }
+        } else if (t >= a.t0 && t < a.t1 && (BM % RPP == 0 || tt0 + r * RPP < BM)) {
             const uint32_t so = (uint32_t)t * out4 + (uint32_t)o0 * 4;
             __builtin_amdgcn_raw_buffer_store_b128(lo, yrs, so, 0, 0);
             __builtin_amdgcn_raw_buffer_store_b128(hi, yrs, so + 16, 0, 0);
@@ -322,8 +360,18 @@ SmallPlan plan_small(const GemmArgs &a, bool grouped, int force_mt, int force_nt
 template <int MT, int NT, bool GROUPED, int D>
 void launch_small_ep(const GemmArgs &a, int grid, int n_mt, int per_xcd, int ntiles, hipStream_t st) {
     const bool bias = a.bias != nullptr;
+    if constexpr (MT == 1 && NT == 8) {
+        if (a.qo) {
+#define VX_SMALLQ(EP)                                                                                             \
+    (bias ? tgemm_small_kernel<MT, NT, GROUPED, D, EP, true, true> : tgemm_small_kernel<MT, NT, GROUPED, D, EP, false, true>)
+            auto k = a.ep == VX_EP_SILU ? VX_SMALLQ(VX_EP_SILU) : VX_SMALLQ(VX_EP_STORE);
+#undef VX_SMALLQ
+            k<<<grid, 256, 0, st>>>(a, n_mt, per_xcd, ntiles);
+            return;
+        }
+    }
 #define VX_SMALL(EP)                                                                                              \
-    (bias ? tgemm_small_kernel<MT, NT, GROUPED, D, EP, true> : tgemm_small_kernel<MT, NT, GROUPED, D, EP, false>)
+    (bias ? tgemm_small_kernel<MT, NT, GROUPED, D, EP, true, false> : tgemm_small_kernel<MT, NT, GROUPED, D, EP, false, false>)
     auto k = a.ep == VX_EP_SILU ? VX_SMALL(VX_EP_SILU) : a.ep == VX_EP_ADD_SCALED ? VX_SMALL(VX_EP_ADD_SCALED)
                                                                                   : VX_SMALL(VX_EP_STORE);
 #undef VX_SMALL
@@ -354,6 +402,26 @@ void launch_small(const GemmArgs &a, const SmallPlan &p, int grid, int n_mt, int
 
 bool gemm_small(const GemmArgs &a, hipStream_t st) {
     const bool grouped = a.ng > 1;
+    if (a.qo) {  // quantized output: 16 x 128 tiles, Store or SiLU, whole tokens from 0
+        if (a.out % 128 != 0 || a.ep == VX_EP_ADD_SCALED || a.m_base != 0 || a.t0 != 0 || a.t1 != a.n) return false;
+        if (a.gs != nullptr || a.r0 != 0 || a.r1 != a.out || a.n > 1024) return false;
+        if (grouped ? (a.spg != 2 || a.ng % 4 != 0 || a.ng > kMaxG) : (a.inp / 64) % 4 != 0) return false;
+        SmallPlan p;
+        p.mt = 1;
+        p.nt = 8;
+        p.tiles = (int)((a.n + 15) / 16 * (a.out / 128));
+        const int steps = (int)(a.inp / 64 / 4);
+        p.d = 1;
+        while (p.d * 2 <= max_ring(1, 8) && steps % (p.d * 2) == 0) p.d *= 2;
+        if (grouped && p.d < 2) return false;
+        const int n_mt = (int)((a.n + 15) / 16), per_xcd = (p.tiles + 7) / 8;
+        if (grouped)
+            launch_small<true>(a, p, 8 * per_xcd, n_mt, per_xcd, p.tiles, st);
+        else
+            launch_small<false>(a, p, 8 * per_xcd, n_mt, per_xcd, p.tiles, st);
+        hip_check(hipGetLastError(), "tgemm_small launch");
+        return true;
+    }
     if (a.gs != nullptr || a.y_bytes == 0 || !a.vec_ok) return false;
     if (a.r0 != 0 || a.r1 != a.out || a.n_base != 0) return false;
     if (grouped ? (a.spg != 2 || a.ng % 4 != 0 || a.ng > kMaxG) : (a.inp / 64) % 4 != 0) return false;

@@ -82,6 +82,16 @@ __device__ inline float exp_poly(float x) {
 __device__ inline float silu_fast(float x) { return x / (1.0f + exp_poly(-x)); }
 __device__ inline float sigmoid_fast(float x) { return 1.0f / (1.0f + exp_poly(-x)); }
 
+// One quantized code (quantize_group_portable, packed.rs:527-535): clamp(rint(x * inv), -127, 127) with
+// round-half-to-even; NaN -> 0 as Rust's `as i8`.
+__device__ inline int8_t code_of(float x, float inv) {
+    float v = __builtin_rintf(x * inv);
+    if (!(v == v)) return 0;
+    v = v < -127.0f ? -127.0f : v;
+    v = v > 127.0f ? 127.0f : v;
+    return (int8_t)(int)v;
+}
+
 // Epilogue::apply (kernels/mod.rs:41-48).
 __device__ inline float ep_apply(int ep, float alpha, float old, float v) {
     if (ep == VX_EP_SILU) return silu_fast(v);

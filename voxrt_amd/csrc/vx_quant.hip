@@ -18,13 +18,6 @@
 
 namespace vx {
 
-__device__ inline int8_t code_of(float x, float inv) {
-    float v = __builtin_rintf(x * inv);
-    if (!(v == v)) return 0;
-    v = v < -127.0f ? -127.0f : v;
-    v = v > 127.0f ? 127.0f : v;
-    return (int8_t)(int)v;
-}
 
 // Mean and 1/sqrt(var + 1e-5) of one row, in the reference's summation order, broadcast to the wavefront.
 __device__ inline void ln_stats(const float *__restrict__ xr, int d, int lane, float &mean, float &inv) {

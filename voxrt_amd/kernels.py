@@ -59,6 +59,7 @@ def lib() -> C.CDLL:
             "vx_tmat_info": (I, [P, C.POINTER(I64), C.POINTER(I64), C.POINTER(I64), C.POINTER(I)]),
             "vx_quantize": (I, [P, I64, I64, I64, P, P, P, P]),
             "vx_gemm_ep": (I, [P, P, P, P, I64, P, P, I, F, P, P]),
+            "vx_gemm_ep_quantize": (I, [P, P, P, P, I64, P, P, I, I64, P, P, P, P]),
             "vx_gemm_rows_range": (I, [P, P, P, P, I64, P, I64, I64, I64, I64, I, F, P]),
             "vx_gemm_single": (I, [P, P, P, P, I64, P, P, P]),
             "vx_quantize_normed": (I, [P, I64, I64, I64, P, P, P, P, P, P]),
@@ -287,6 +288,35 @@ def gemm_ep(w: TernaryMatrix, x: QuantAct, y, bias=None, ep: Epilogue = Epilogue
                            _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), x.n, _dev_ptr(y, torch.float32, "y"),
                            _dev_ptr(bias, torch.float32, "bias"), ep.kind, ep.alpha,
                            _dev_ptr(group_sums, torch.int32, "group_sums"), _stream(stream)))
+
+
+def gemm_ep_quantize(w: TernaryMatrix, x: QuantAct, bias=None, ep: Epilogue = Epilogue.Silu, group: int = 128,
+                     y_tmp=None, stream=None) -> QuantAct:
+    """The FFN up-projection with the next GEMM's quantization fused (encoder.rs:87-89: forward_prepared_ep into
+    hbuf, then prepare(hbuf)): QuantAct of ep(x . w^T) (+ bias) in `group`-column groups, equal to gemm_ep followed
+    by QuantAct.quantize. y_tmp float32 [n, out] is scratch for shapes the fused epilogue does not take (allocated
+    here when None)."""
+    import torch
+
+    if x.inp != w.inp or x.group != w.group:
+        raise ValueError("activation and weight shapes or groups differ")
+    if ep.kind not in (Epilogue.Store.kind, Epilogue.Silu.kind):
+        raise ValueError("a quantized output takes the Store or Silu epilogue")
+    if group <= 0 or w.out % group:
+        raise ValueError("out must be a multiple of group")
+    dev = x.x.device
+    n = x.n
+    if y_tmp is None and not (group == 128 and n <= 1024 and w.out % 128 == 0):
+        y_tmp = torch.empty((n, w.out), dtype=torch.float32, device=dev)
+    q = torch.empty((n, w.out), dtype=torch.int8, device=dev)
+    s = torch.empty((w.out // group, npad(n)), dtype=torch.float32, device=dev)
+    g = torch.empty((w.out // group, npad(n)), dtype=torch.int32, device=dev)
+    check(lib().vx_gemm_ep_quantize(w._h, _dev_ptr(x.x, torch.int8, "x"), _dev_ptr(x.scales_t, torch.float32, "scales_t"),
+                                    _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), n, _dev_ptr(y_tmp, torch.float32, "y_tmp"),
+                                    _dev_ptr(bias, torch.float32, "bias"), ep.kind, group,
+                                    _dev_ptr(q, torch.int8, "q"), _dev_ptr(s, torch.float32, "scales_t"),
+                                    _dev_ptr(g, torch.int32, "gsum_t"), _stream(stream)))
+    return QuantAct(q, s, g, n, w.out, group)
 
 
 def gemm(w: TernaryMatrix, x: QuantAct, y, bias=None, stream=None) -> None:
