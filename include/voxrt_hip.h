@@ -16,6 +16,7 @@
  *   vx_quantize_normed                <- TernaryLinear::prepare_normed (ternary_linear.rs:132-155)
  *   vx_layer_norm                     <- tensor::layer_norm (tensor.rs:700-719)
  *   vx_glu_dwconv_silu, vx_fold_bn    <- ConvModule::forward_fused / load (encoder.rs:548-573, 590-624)
+ *   vx_glu_dwconv_silu_quantize       <- the same conv rows + pw2.prepare(hb) (encoder.rs:605-625)
  *   vx_linear_f32                     <- tensor::linear (tensor.rs:98-127)
  *   vx_subsampling*                   <- Subsampling::forward / out_frames (subsampling.rs:114-204)
  *   vx_rel_pos_table                  <- encoder::rel_pos_table (encoder.rs:760-776)
@@ -137,6 +138,14 @@ vx_status vx_layer_norm(const float *x, int64_t n, int64_t d, const float *gamma
  * halves of g, taps outside [0, t) skipped. w_t [k][d] and bias [d] are the BatchNorm-folded taps of vx_fold_bn. */
 vx_status vx_glu_dwconv_silu(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t, const float *bias,
                              float *out, void *stream);
+
+/* glu_dwconv_silu + prepare fused (ConvModule::forward_fused, encoder.rs:605-625: the depthwise conv rows, then
+ * pw2.prepare(hb)): the rows of vx_glu_dwconv_silu quantized in 128-channel groups (group must be 128, d a
+ * multiple of 256) into q int8 [t, d], scales_t float32 and gsum_t int32 [d/128, VX_NPAD(t)] (pad tokens zero),
+ * bit for bit as vx_glu_dwconv_silu followed by vx_quantize. */
+vx_status vx_glu_dwconv_silu_quantize(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t,
+                                      const float *bias, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t,
+                                      void *stream);
 
 /* HOST: fold BatchNorm(eval) into the depthwise taps: dw [d][k] (PyTorch [d,1,k]) -> w_t [k][d], bias [d]. */
 vx_status vx_fold_bn(const float *dw, const float *gamma, const float *beta, const float *mean, const float *var,

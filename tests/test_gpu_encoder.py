@@ -291,3 +291,28 @@ def test_encoder_batch_of_32_equals_single_segments(dev):
         _bits_equal(got[s], one, f"batch of 32, segment {s}")
     torch.cuda.synchronize()
     enc.free()
+
+
+@pytest.mark.parametrize("t", [1, 29, 338, 750])
+def test_glu_dwconv_silu_quantize_equals_oracle(dev, orc, t):
+    """The conv rows quantized for pointwise_conv2 in the same kernel (encoder.rs:605-625) equal the oracle's
+    dwconv_bn_silu(glu(g)) quantized in 128-channel groups: codes, scales and code sums bit for bit, pad tokens
+    zero."""
+    import torch
+
+    from voxrt_amd import encoder as E
+
+    d = 1024
+    g = _x(t + 7, t, 2 * d, scale=2.0)
+    dw = _x(20, d, 9, scale=0.3)
+    gamma, beta, mean = _x(21, d) * 0.1 + 1, _x(22, d) * 0.1, _x(23, d) * 0.1
+    var = np.random.default_rng(24).uniform(0.5, 1.5, d).astype(np.float32)
+    w_t, bias = orc.fold_bn(dw, gamma, beta, mean, var)
+    wq, ws, wg = orc.quantize(orc.dwconv_bn_silu(orc.glu(g), w_t, bias), 128)
+    got = E.glu_dwconv_silu_quantize(_t(g, dev), _t(w_t, dev), _t(bias, dev))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.x.cpu().numpy(), wq, err_msg=f"codes t={t}")
+    st, gt = got.scales_t.cpu().numpy(), got.gsum_t.cpu().numpy()
+    _bits_equal(st[:, :t].T.copy(), ws, f"scales t={t}")
+    np.testing.assert_array_equal(gt[:, :t].T, wg, err_msg=f"gsum t={t}")
+    assert not st[:, t:].any() and not gt[:, t:].any(), f"pad tokens not zero t={t}"

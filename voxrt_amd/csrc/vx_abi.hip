@@ -24,6 +24,8 @@ void gemm_quant(const TMat *w, const int8_t *xq, const float *xs_t, const int32_
 void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y, hipStream_t stream);
 void glu_dwconv_silu(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t, const float *bias, float *out,
                      hipStream_t st);
+void glu_dwconv_silu_quant_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
+                               const float *bias, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st);
 void linear_f32(const float *x, int64_t n, int64_t in_f, const float *w, const float *b, int64_t out_f, float *y,
                 bool relu, hipStream_t st);
 int64_t subsampling(const float *feats, int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s, const float *conv0_w,
@@ -213,6 +215,15 @@ vx_status vx_layer_norm(const float *x, int64_t n, int64_t d, const float *gamma
 vx_status vx_glu_dwconv_silu(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t, const float *bias,
                              float *out, void *stream) {
     return guarded([&] { vx::glu_dwconv_silu(g, t, d, k, w_t, bias, out, (hipStream_t)stream); });
+}
+
+vx_status vx_glu_dwconv_silu_quantize(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t,
+                                      const float *bias, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t,
+                                      void *stream) {
+    return guarded([&] {
+        vx::require(group == 128, "glu_dwconv_quantize: 128-channel groups");
+        vx::glu_dwconv_silu_quant_seg(g, 1, t, d, k, w_t, bias, q, scales_t, gsum_t, (hipStream_t)stream);
+    });
 }
 
 vx_status vx_fold_bn(const float *dw, const float *gamma, const float *beta, const float *mean, const float *var,

@@ -37,6 +37,8 @@ void gemm_quant(const TMat *w, const int8_t *xq, const float *xs_t, const int32_
 void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y, hipStream_t stream);
 void glu_dwconv_silu_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
                          const float *bias, float *out, hipStream_t st);
+void glu_dwconv_silu_quant_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
+                               const float *bias, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st);
 int64_t subsampling_seg(const float *feats, int64_t nseg, int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s,
                         const float *conv0_w, const float *conv0_b, const float *dw_w, const float *dw_b,
                         const float *pw_w, const float *pw_b, const float *lin_w, const float *lin_b,
@@ -224,9 +226,15 @@ void run_layers(vx_encoder *e, EncWs &w, hipStream_t st) {
         // convolution module
         lnq(2);
         gemm_full(L.lin[5], w.a, t, w.g2.as<float>(), VX_EP_STORE, 0.0f, st);
-        glu_dwconv_silu_seg(w.g2.as<float>(), w.nseg, w.t, d, c.kconv, L.dw_t.as<float>(), L.dw_bias.as<float>(),
-                            w.hb.as<float>(), st);
-        quant(w.hb.as<float>(), d, w.a);
+        if (G == 128 && d % 256 == 0) {  // the conv rows quantized for pw2 in the same kernel
+            glu_dwconv_silu_quant_seg(w.g2.as<float>(), w.nseg, w.t, d, c.kconv, L.dw_t.as<float>(),
+                                      L.dw_bias.as<float>(), w.a.q.as<int8_t>(), w.a.s.as<float>(), w.a.g.as<int32_t>(),
+                                      st);
+        } else {
+            glu_dwconv_silu_seg(w.g2.as<float>(), w.nseg, w.t, d, c.kconv, L.dw_t.as<float>(), L.dw_bias.as<float>(),
+                                w.hb.as<float>(), st);
+            quant(w.hb.as<float>(), d, w.a);
+        }
         gemm_full(L.lin[6], w.a, t, x, VX_EP_ADD_SCALED, 1.0f, st);
         ffn(3, 7, 8);
         layer_norm(x, t, d, L.ln_g[4].as<float>(), L.ln_b[4].as<float>(), xn, st);

@@ -53,6 +53,74 @@ void glu_dwconv_silu_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int
     hip_check(hipGetLastError(), "glu_dwconv kernel launch");
 }
 
+// As glu_dwconv_silu_kernel, with the result quantized for pointwise_conv2 (ConvModule::forward_fused,
+// encoder.rs:605-625: the conv rows, then pw2.prepare(hb) = QuantAct::quantize_layout, packed.rs:307-436) in
+// 128-channel groups, so hb never reaches memory. A block is 256 channels of one row: two groups of two wavefronts
+// each; a group's amax and code sum meet in LDS (a max and an integer sum are exact in any order). Rows [n, np)
+// are the pad tokens: their scales and code sums are written as zero.
+__global__ __launch_bounds__(256) void glu_dwconv_silu_quant_kernel(const float *__restrict__ g, int t, int n, int np,
+                                                                   int d, int k, const float *__restrict__ w_t,
+                                                                   const float *__restrict__ bias,
+                                                                   int8_t *__restrict__ q, float *__restrict__ st,
+                                                                   int32_t *__restrict__ gt) {
+    __shared__ float smax[4];
+    __shared__ int ssum[4];
+    const int c = blockIdx.x * 256 + threadIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int row = blockIdx.y;
+    const int64_t gi = (int64_t)(c / 128) * np + row;
+    if (row >= n) {  // uniform per block
+        if ((threadIdx.x & 127) == 0) {
+            st[gi] = 0.0f;
+            gt[gi] = 0;
+        }
+        return;
+    }
+    const int i = row % t, base = row - i, pad = (k - 1) / 2;
+    float acc = bias[c];
+    for (int kk = 0; kk < k; kk++) {
+        const int j = i + kk - pad;
+        if (j < 0 || j >= t) continue;
+        const float *gj = g + (int64_t)(base + j) * 2 * d;
+        const float a = gj[c] * sigmoid_fast(gj[d + c]);
+        acc = acc + w_t[(int64_t)kk * d + c] * a;
+    }
+    const float v = silu_fast(acc);
+    float m = fabsf(v);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (lane == 0) smax[wv] = m;
+    __syncthreads();
+    m = fmaxf(smax[wv & ~1], smax[wv | 1]);
+    const float s = m == 0.0f ? 1.0f : m / 127.0f;
+    const float inv = 1.0f / s;
+    const int8_t code = code_of(v, inv);
+    q[(int64_t)row * d + c] = code;
+    int sum = code;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    if (lane == 0) ssum[wv] = sum;
+    __syncthreads();
+    if ((threadIdx.x & 127) == 0) {
+        st[gi] = s;
+        gt[gi] = ssum[wv] + ssum[wv + 1];
+    }
+}
+
+// nseg segments of t frames: g [nseg][t][2d] -> the QuantAct of the conv rows in 128-channel groups: q int8
+// [nseg * t][d], scales_t and gsum_t [d / 128][npad(nseg * t)].
+void glu_dwconv_silu_quant_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
+                               const float *bias, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st) {
+    require(g && w_t && bias && q && scales_t && gsum_t, "glu_dwconv_quantize: NULL pointer");
+    require(nseg >= 1 && t >= 0 && d > 0 && d % 256 == 0 && k > 0 && k % 2 == 1 && nseg * t * 2 * d < (1ll << 31) &&
+                nseg * t <= 65535,
+            "glu_dwconv_quantize: bad shape (d a multiple of 256)");
+    if (t == 0) return;
+    const int64_t n = nseg * t, np = (n + 15) / 16 * 16;
+    glu_dwconv_silu_quant_kernel<<<dim3((unsigned)(d / 256), (unsigned)np), 256, 0, st>>>(
+        g, (int)t, (int)n, (int)np, (int)d, (int)k, w_t, bias, q, scales_t, gsum_t);
+    hip_check(hipGetLastError(), "glu_dwconv_quantize kernel launch");
+}
+
 void glu_dwconv_silu(const float *g, int64_t t, int64_t d, int64_t k, const float *w_t, const float *bias, float *out,
                      hipStream_t st) {
     require(t <= 65535, "glu_dwconv: t <= 65535");

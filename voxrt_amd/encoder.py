@@ -115,6 +115,22 @@ def glu_dwconv_silu(g, w_t, bias, out=None):
     return out
 
 
+def glu_dwconv_silu_quantize(g, w_t, bias, group=128):
+    """glu_dwconv_silu followed by pw2.prepare (encoder.rs:605-625) in one kernel: the QuantAct of the conv rows in
+    128-channel groups."""
+    import torch
+
+    t, d2 = g.shape
+    d, k = d2 // 2, w_t.shape[0]
+    q = torch.empty((t, d), dtype=torch.int8, device=g.device)
+    s = torch.empty((d // group, K.npad(t)), dtype=torch.float32, device=g.device)
+    gs = torch.empty((d // group, K.npad(t)), dtype=torch.int32, device=g.device)
+    check(lib().vx_glu_dwconv_silu_quantize(_f32(g, "g"), t, d, k, _f32(w_t, "w_t"), _f32(bias, "bias"), group,
+                                            K._dev_ptr(q, torch.int8, "q"), _f32(s, "scales_t"),
+                                            K._dev_ptr(gs, torch.int32, "gsum_t"), K._stream()))
+    return K.QuantAct(q, s, gs, t, d, group)
+
+
 def linear_f32(x, w, b=None, relu=False, y=None):
     import torch
 

@@ -65,6 +65,7 @@ def lib() -> C.CDLL:
             "vx_quantize_normed": (I, [P, I64, I64, I64, P, P, P, P, P, P]),
             "vx_layer_norm": (I, [P, I64, I64, P, P, P, P]),
             "vx_glu_dwconv_silu": (I, [P, I64, I64, I64, P, P, P, P]),
+            "vx_glu_dwconv_silu_quantize": (I, [P, I64, I64, I64, P, P, I64, P, P, P, P]),
             "vx_fold_bn": (I, [P, P, P, P, P, I64, I64, P, P]),
             "vx_linear_f32": (I, [P, I64, I64, P, P, I64, P, I, P]),
             "vx_subsampling_frames": (I64, [I64, I64, I64]),
