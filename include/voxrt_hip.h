@@ -179,6 +179,14 @@ vx_status vx_attention_core(const float *qkv, const float *rel_k, int64_t t, int
                             const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
                             void *stream);
 
+/* attention core + prepare fused (Attention::forward_fused, encoder.rs:180-183: attn_core_int8 into ctx, then
+ * wo.prepare(ctx)): as vx_attention_core, but ctx is written as the o-projection's int8 activations in 128-column
+ * groups, one per head (group must be 128): q int8 [t, d], scales_t float32 and gsum_t int32 [h, VX_NPAD(t)]
+ * (pad tokens zero), bit for bit as vx_attention_core followed by vx_quantize. */
+vx_status vx_attention_core_quantize(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h,
+                                     const float *bias_u, const float *bias_v, float scaling, void *ws, int64_t group,
+                                     int8_t *q, float *scales_t, int32_t *gsum_t, void *stream);
+
 /* ---------------------------------------------------------------------------------------------- encoder */
 
 /* Shape of a FastConformer encoder (reference/config.json encoder_config): d = heads * 128. */

@@ -316,3 +316,25 @@ def test_glu_dwconv_silu_quantize_equals_oracle(dev, orc, t):
     _bits_equal(st[:, :t].T.copy(), ws, f"scales t={t}")
     np.testing.assert_array_equal(gt[:, :t].T, wg, err_msg=f"gsum t={t}")
     assert not st[:, t:].any() and not gt[:, t:].any(), f"pad tokens not zero t={t}"
+
+
+@pytest.mark.parametrize("t,heads", [(1, 8), (29, 8), (338, 8), (750, 2)])
+def test_attention_core_quantize_equals_oracle(dev, orc, t, heads):
+    """The attention core writing the o-projection's activations (encoder.rs:180-183) equals the oracle's
+    attn_core_int8 quantized in 128-column groups: codes, scales and code sums bit for bit, pad tokens zero."""
+    import torch
+
+    from voxrt_amd import encoder as E
+
+    d = heads * 128
+    qkv = _x(29 + t, t, 3 * d)
+    rel = _x(30 + t, 2 * t - 1, d)
+    bu, bv = _x(31, heads, 128, scale=0.3), _x(32, heads, 128, scale=0.3)
+    wq, ws, wg = orc.quantize(orc.attn_core_int8(qkv, rel, heads, bu, bv), 128)
+    got = E.attention_core_quantize(_t(qkv, dev), _t(rel, dev), heads, _t(bu, dev), _t(bv, dev))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.x.cpu().numpy(), wq, err_msg=f"codes t={t}")
+    st, gt = got.scales_t.cpu().numpy(), got.gsum_t.cpu().numpy()
+    _bits_equal(st[:, :t].T.copy(), ws, f"scales t={t}")
+    np.testing.assert_array_equal(gt[:, :t].T, wg, err_msg=f"gsum t={t}")
+    assert not st[:, t:].any() and not gt[:, t:].any(), f"pad tokens not zero t={t}"

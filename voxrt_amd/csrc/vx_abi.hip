@@ -40,6 +40,9 @@ void rel_pos_table(int64_t t, int64_t d, float *out);
 size_t attn_ws_bytes(int64_t t, int64_t d, int64_t h);
 void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h, const float *bias_u,
                     const float *bias_v, float scaling, void *ws, float *ctx, hipStream_t st);
+void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
+                        const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
+                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t);
 vx_encoder *encoder_create(const vx_encoder_config *cfg);
 void encoder_free(vx_encoder *e);
 void encoder_use_graphs(vx_encoder *e, bool on);
@@ -274,6 +277,17 @@ vx_status vx_attention_core(const float *qkv, const float *rel_k, int64_t t, int
                             void *stream) {
     return guarded([&] {
         vx::attention_core(qkv, rel_k, t, d, h, bias_u, bias_v, scaling, ws, ctx, (hipStream_t)stream);
+    });
+}
+
+vx_status vx_attention_core_quantize(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h,
+                                     const float *bias_u, const float *bias_v, float scaling, void *ws, int64_t group,
+                                     int8_t *q, float *scales_t, int32_t *gsum_t, void *stream) {
+    return guarded([&] {
+        vx::require(group == 128, "attention quantized output: 128-column groups (one per head)");
+        vx::require(q && scales_t && gsum_t, "q, scales_t and gsum_t must not be NULL");
+        vx::attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, ws, nullptr, (hipStream_t)stream, q,
+                               scales_t, gsum_t);
     });
 }
 

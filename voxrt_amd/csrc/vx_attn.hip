@@ -140,16 +140,28 @@ __host__ __device__ inline int s1w_of(int t) { return up16(t) + 4; }
 // the band of a block spans at most t + 45 positions after its start is rounded down to a 16-block
 __host__ __device__ inline int s2w_of(int t) { return up16(t + 48) + 4; }
 __host__ __device__ inline size_t core_lds_bytes(int t) {
-    return (size_t)16 * s1w_of(t) * 4 + (size_t)16 * s2w_of(t) * 4 + (size_t)16 * up64(t) + 64 * 4;
+    return (size_t)16 * s1w_of(t) * 4 + (size_t)16 * s2w_of(t) * 4 + (size_t)16 * up64(t) + 192 * 4;
 }
 
-__global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, float scaling, float *__restrict__ ctx) {
+// ctx written as the o-projection's int8 activations (Attention::forward_fused, encoder.rs:180-183: attn_core_int8
+// into ctx, then wo.prepare(ctx) = QuantAct::quantize_layout, packed.rs:307-436): a head's 128 channels are one
+// 128-column group, so each query row's group is complete inside the workgroup.
+struct AttnQOut {
+    int8_t *q;     // [nseg * t][d]
+    float *s;      // scales_t [h][np]
+    int32_t *g;    // gsum_t [h][np]
+    int np;        // npad(nseg * t)
+};
+
+template <bool QOUT>
+__global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, float scaling, float *__restrict__ ctx,
+                                                        AttnQOut Q) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int s1w = s1w_of(D.t), s2w = s2w_of(D.t);
     float *s1 = (float *)smem;
     float *s2 = s1 + 16 * s1w;
     int8_t *pq = (int8_t *)(s2 + 16 * s2w);
-    float *rowv = (float *)(pq + 16 * D.tv);  // [0,16) max, [16,32) 1/sum, [32,48) prob scale
+    float *rowv = (float *)(pq + 16 * D.tv);  // [0,16) max, [16,32) 1/sum, [32,48) prob scale, [64,192) QOUT
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.y, i0 = blockIdx.x * 16;
     const int t = D.t;
@@ -164,8 +176,9 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
         W.ks += so;
         W.vq += seg * D.h * kDh * D.tv;
         W.vs += seg * D.h * kDh;
-        ctx += seg * D.t * D.d;
+        if (!QOUT) ctx += seg * D.t * D.d;
     }
+    const int64_t row0 = (int64_t)blockIdx.z * D.t;  // this segment's first token row
     const int imax = min(i0 + 15, t - 1);
     const int pb0 = (t - 1 - imax) & ~15;        // first position block of the band
     const int pend = 2 * t - 2 - i0;             // last position used by the block
@@ -270,7 +283,10 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
     }
     __syncthreads();
     // context: channel blocks 2*wave, 2*wave+1; K over tv in 64-steps; A = pq rows from LDS, B = vT rows
-    for (int cb = 2 * wave; cb < 2 * wave + 2; cb++) {
+    float val[2][4];
+#pragma unroll
+    for (int cbi = 0; cbi < 2; cbi++) {
+        const int cb = 2 * wave + cbi;
         v4i acc = {0, 0, 0, 0};
         const int8_t *vr = W.vq + ((int64_t)h * kDh + cb * 16 + arow) * D.tv + 16 * aq;
         const int8_t *pr = pq + arow * D.tv + 16 * aq;
@@ -284,8 +300,59 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int r = drow + e;
-            if (r < nrows)
-                ctx[(int64_t)(i0 + r) * D.d + h * kDh + c] = __builtin_fmaf((float)acc[e], rowv[32 + r] * vsv, 0.0f);
+            val[cbi][e] = __builtin_fmaf((float)acc[e], rowv[32 + r] * vsv, 0.0f);
+            if (!QOUT && r < nrows) ctx[(int64_t)(i0 + r) * D.d + h * kDh + c] = val[cbi][e];
+        }
+    }
+    if constexpr (QOUT) {
+        // quantize_group of each query row over the head's 128 channels: 2 per lane, 16 lanes per wave, 4 waves
+        float *qmax = rowv + 64;       // [wave][row]
+        int *qsum = (int *)(rowv + 128);
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float m = fmaxf(fabsf(val[0][e]), fabsf(val[1][e]));
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            if (dcol == 0) qmax[wave * 16 + drow + e] = m;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int r = drow + e;
+            const float m = fmaxf(fmaxf(qmax[r], qmax[16 + r]), fmaxf(qmax[32 + r], qmax[48 + r]));
+            sc[e] = m == 0.0f ? 1.0f : m / 127.0f;
+            const float inv = 1.0f / sc[e];
+            const int8_t c0 = q_code(val[0][e], inv), c1 = q_code(val[1][e], inv);
+            if (r < nrows) {
+                int8_t *qr = Q.q + (row0 + i0 + r) * D.d + h * kDh + 2 * wave * 16 + dcol;
+                qr[0] = c0;
+                qr[16] = c1;
+            }
+            int sum = (int)c0 + (int)c1;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            if (dcol == 0) qsum[wave * 16 + r] = sum;
+        }
+        __syncthreads();
+        if (wave == 0 && dcol == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int r = drow + e;
+                if (r < nrows) {
+                    const int64_t gi = (int64_t)h * Q.np + row0 + i0 + r;
+                    Q.s[gi] = sc[e];
+                    Q.g[gi] = qsum[r] + qsum[16 + r] + qsum[32 + r] + qsum[48 + r];
+                }
+            }
+        }
+        // pad tokens [nseg * t, np) of this head's group: zero scale and code sum
+        if (blockIdx.x == gridDim.x - 1 && blockIdx.z == gridDim.z - 1) {
+            const int64_t n = (int64_t)gridDim.z * D.t;
+            if (tid < Q.np - n) {
+                Q.s[(int64_t)h * Q.np + n + tid] = 0.0f;
+                Q.g[(int64_t)h * Q.np + n + tid] = 0;
+            }
         }
     }
 }
@@ -312,10 +379,14 @@ size_t attn_ws_bytes(int64_t t, int64_t d, int64_t h) { return attn_ws_bytes_seg
 
 // ctx [nseg][t][d] from qkv [nseg][t][3d] (q | k | v) and the shared rel_k [2t-1][d] of t frames: each segment's
 // attention on its own tokens; ws is attn_ws_bytes_seg(t, d, h, nseg) device bytes.
+// With q (and scales_t, gsum_t) not NULL, ctx is not written: the o-projection's activations are, in 128-column
+// groups (one per head): q int8 [nseg * t][d], scales_t and gsum_t [h][npad(nseg * t)].
 void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
                         const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
-                        hipStream_t st) {
-    require(qkv && rel_k && bias_u && bias_v && ws && ctx, "attention: NULL pointer");
+                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t) {
+    const bool qout = q != nullptr;
+    require(qkv && rel_k && bias_u && bias_v && ws && (ctx || qout) && (!qout || (scales_t && gsum_t)),
+            "attention: NULL pointer");
     require(h > 0 && d == h * kDh, "attention: the head dimension must be 128");
     require(t >= 1 && t <= 1024, "attention: 1 <= t <= 1024 frames");
     require(nseg >= 1 && nseg <= 65535 && nseg * t * 3 * d < (1ll << 31), "attention: 1 <= segments, size < 2^31");
@@ -347,20 +418,27 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
     const size_t lds = core_lds_bytes((int)t);
     static bool lds_raised = false;
     if (!lds_raised) {
-        hip_check(hipFuncSetAttribute((const void *)attn_core_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      160 * 1024),
+        hip_check(hipFuncSetAttribute((const void *)attn_core_kernel<false>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
+                  "attention LDS limit");
+        hip_check(hipFuncSetAttribute((const void *)attn_core_kernel<true>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
                   "attention LDS limit");
         lds_raised = true;
     }
-    attn_core_kernel<<<dim3((unsigned)(D.tp / 16), (unsigned)h, (unsigned)nseg), 256, lds, st>>>(D, W, scaling,
-                                                                                                    ctx);
+    AttnQOut Q{q, scales_t, gsum_t, (int)((nseg * t + 15) / 16 * 16)};
+    const dim3 grid((unsigned)(D.tp / 16), (unsigned)h, (unsigned)nseg);
+    if (qout)
+        attn_core_kernel<true><<<grid, 256, lds, st>>>(D, W, scaling, ctx, Q);
+    else
+        attn_core_kernel<false><<<grid, 256, lds, st>>>(D, W, scaling, ctx, Q);
     hip_check(hipGetLastError(), "attention core kernel launch");
 }
 
 // ctx [t][d] from qkv [t][3d] (q | k | v) and rel_k [2t-1][d]; ws is attn_ws_bytes(t, d, h) device bytes.
 void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h, const float *bias_u,
                     const float *bias_v, float scaling, void *ws, float *ctx, hipStream_t st) {
-    attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, ws, ctx, st);
+    attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, ws, ctx, st, nullptr, nullptr, nullptr);
 }
 
 }  // namespace vx

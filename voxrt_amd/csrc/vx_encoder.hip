@@ -11,7 +11,9 @@
 //   per layer, in place on the residual stream x [t][d] (ConformerLayer::forward_profiled, encoder.rs:706-756):
 //     ff1:  q = LNquant(x); h = silu(W1 q); x = fma(0.5, W2 quant(h), x)   (W1's GEMM writes quant(h) itself)
 //     attn: q = LNquant(x); qkv = Wqkv q; rel = Wpos quant(pos); ctx = core(qkv, rel); x = fma(1, Wo quant(ctx), x)
+//           (the core writes quant(ctx) itself)
 //     conv: q = LNquant(x); g = Wpw1 q; hb = silu(dwconv_bn(glu(g))); x = fma(1, Wpw2 quant(hb), x)
+//           (the depthwise-conv kernel writes quant(hb) itself)
 //     ff2 as ff1; x' = LN_out(x) into the other half of a ping-pong pair.
 //   All of it is stream-ordered kernels on device buffers; with graphs on, the layer stack of each t is captured
 //   once into a hipGraph and replayed (no memset nodes are recorded: every buffer is written by a kernel).
@@ -51,7 +53,7 @@ void rel_pos_table(int64_t t, int64_t d, float *out);
 size_t attn_ws_bytes_seg(int64_t t, int64_t d, int64_t h, int64_t nseg);
 void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
                         const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
-                        hipStream_t st);
+                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t);
 
 namespace {
 
@@ -219,9 +221,16 @@ void run_layers(vx_encoder *e, EncWs &w, hipStream_t st) {
         lnq(1);
         gemm_full(L.lin[2], w.a, t, w.qkv.as<float>(), VX_EP_STORE, 0.0f, st);
         gemm_full(L.lin[4], w.posq, w.np, w.rel_k.as<float>(), VX_EP_STORE, 0.0f, st);
-        attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>(), w.nseg, w.t, d, c.heads, L.bias_u.as<float>(),
-                           L.bias_v.as<float>(), scaling, w.attn.p, w.ctx.as<float>(), st);
-        quant(w.ctx.as<float>(), d, w.a);
+        if (G == 128) {  // a head's 128 channels are one group: the core writes the o-projection's activations
+            attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>(), w.nseg, w.t, d, c.heads, L.bias_u.as<float>(),
+                               L.bias_v.as<float>(), scaling, w.attn.p, nullptr, st, w.a.q.as<int8_t>(),
+                               w.a.s.as<float>(), w.a.g.as<int32_t>());
+        } else {
+            attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>(), w.nseg, w.t, d, c.heads, L.bias_u.as<float>(),
+                               L.bias_v.as<float>(), scaling, w.attn.p, w.ctx.as<float>(), st, nullptr, nullptr,
+                               nullptr);
+            quant(w.ctx.as<float>(), d, w.a);
+        }
         gemm_full(L.lin[3], w.a, t, x, VX_EP_ADD_SCALED, 1.0f, st);
         // convolution module
         lnq(2);

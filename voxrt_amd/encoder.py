@@ -172,6 +172,28 @@ def attention_core(qkv, rel_k, heads, bias_u, bias_v, ctx=None, ws=None):
     return ctx
 
 
+def attention_core_quantize(qkv, rel_k, heads, bias_u, bias_v, group=128, ws=None):
+    """attention_core followed by wo.prepare (encoder.rs:180-183) in one kernel: the QuantAct of ctx in 128-column
+    groups, one per head."""
+    import torch
+
+    t, d3 = qkv.shape
+    d = d3 // 3
+    nb = attention_ws_bytes(t, d, heads)
+    if nb < 0:
+        raise ValueError("attention: d must be heads * 128")
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=qkv.device) if ws is None else ws
+    scaling = float(np.float32(1.0) / np.sqrt(np.float32(d // heads)))
+    q = torch.empty((t, d), dtype=torch.int8, device=qkv.device)
+    s = torch.empty((d // group, K.npad(t)), dtype=torch.float32, device=qkv.device)
+    gs = torch.empty((d // group, K.npad(t)), dtype=torch.int32, device=qkv.device)
+    check(lib().vx_attention_core_quantize(_f32(qkv, "qkv"), _f32(rel_k, "rel_k"), t, d, heads,
+                                           _f32(bias_u, "bias_u"), _f32(bias_v, "bias_v"), scaling,
+                                           C.c_void_p(ws.data_ptr()), group, K._dev_ptr(q, torch.int8, "q"),
+                                           _f32(s, "scales_t"), K._dev_ptr(gs, torch.int32, "gsum_t"), K._stream()))
+    return K.QuantAct(q, s, gs, t, d, group)
+
+
 SUB_KEYS = ("conv0_w", "conv0_b", "dw_w", "dw_b", "pw_w", "pw_b", "lin_w", "lin_b")
 
 
