@@ -199,56 +199,77 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
         qus[e] = W.qus[h * D.tp + i0 + drow + e];
         qvs[e] = W.qvs[h * D.tp + i0 + drow + e];
     }
-    // content scores: key block kb -> s1[row][16*kb + col]
-    for (int kb = wave; kb < nkb; kb += 4) {
-        const int8_t *kr = W.kq + ((int64_t)h * D.tp + kb * 16 + arow) * kDh + 16 * aq;
-        const v4i b0 = *(const v4i *)kr, b1 = *(const v4i *)(kr + 64);
-        v4i acc = {0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au0, b0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au1, b1, acc, 0, 0, 0);
-        const float ksv = W.ks[h * D.tp + kb * 16 + dcol];
+    // content scores: key block kb -> s1[row][16*kb + col]. A wave takes blocks wave, wave+4, ...; the loads of
+    // kPF of its blocks are issued before their MFMAs (past the last block: a repeat of it, not used)
+    constexpr int kPF = 4;
+    for (int kb0 = wave; kb0 < nkb; kb0 += 4 * kPF) {
+        v4i b0[kPF], b1[kPF];
+        float ksv[kPF];
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            s1[(drow + e) * s1w + kb * 16 + dcol] = __builtin_fmaf((float)acc[e], qus[e] * ksv, 0.0f);
-    }
-    // position band: block pb -> s2[row][16*pb' + col], position pb0 + 16*pb' + col
-    for (int pb = wave; pb < npb; pb += 4) {
-        const int p0 = pb0 + pb * 16;
-        const int8_t *rr = W.rq + ((int64_t)h * D.rp + p0 + arow) * kDh + 16 * aq;
-        const v4i b0 = *(const v4i *)rr, b1 = *(const v4i *)(rr + 64);
-        v4i acc = {0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1, acc, 0, 0, 0);
-        const float rsv = W.rs[h * D.rp + p0 + dcol];
+        for (int p = 0; p < kPF; p++) {
+            const int kb = min(kb0 + 4 * p, nkb - 1);
+            const int8_t *kr = W.kq + ((int64_t)h * D.tp + kb * 16 + arow) * kDh + 16 * aq;
+            b0[p] = *(const v4i *)kr;
+            b1[p] = *(const v4i *)(kr + 64);
+            ksv[p] = W.ks[h * D.tp + kb * 16 + dcol];
+        }
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            s2[(drow + e) * s2w + pb * 16 + dcol] = __builtin_fmaf((float)acc[e], qvs[e] * rsv, 0.0f);
+        for (int p = 0; p < kPF; p++) {
+            const int kb = kb0 + 4 * p;
+            if (kb < nkb) {
+                v4i acc = {0, 0, 0, 0};
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au0, b0[p], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au1, b1[p], acc, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    s1[(drow + e) * s1w + kb * 16 + dcol] = __builtin_fmaf((float)acc[e], qus[e] * ksv[p], 0.0f);
+            }
+        }
     }
-    __syncthreads();
-    const int nrows = imax - i0 + 1;  // valid query rows of the block
-    // score = S1 + S2[t-1-i+j], in place in s1
-    for (int e = tid; e < 16 * t; e += 256) {
-        const int r = e / t, j = e % t;
-        if (r < nrows) {
-            const int i = i0 + r;
-            s1[r * s1w + j] = s1[r * s1w + j] + s2[r * s2w + (t - 1 - i + j - pb0)];
+    // position band: block pb -> s2[row][16*pb' + col], position pb0 + 16*pb' + col (loads ahead as above)
+    for (int q0 = wave; q0 < npb; q0 += 4 * kPF) {
+        v4i b0[kPF], b1[kPF];
+        float rsv[kPF];
+#pragma unroll
+        for (int p = 0; p < kPF; p++) {
+            const int p0 = pb0 + min(q0 + 4 * p, npb - 1) * 16;
+            const int8_t *rr = W.rq + ((int64_t)h * D.rp + p0 + arow) * kDh + 16 * aq;
+            b0[p] = *(const v4i *)rr;
+            b1[p] = *(const v4i *)(rr + 64);
+            rsv[p] = W.rs[h * D.rp + p0 + dcol];
+        }
+#pragma unroll
+        for (int p = 0; p < kPF; p++) {
+            const int pb = q0 + 4 * p;
+            if (pb < npb) {
+                v4i acc = {0, 0, 0, 0};
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0[p], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1[p], acc, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    s2[(drow + e) * s2w + pb * 16 + dcol] = __builtin_fmaf((float)acc[e], qvs[e] * rsv[p], 0.0f);
+            }
         }
     }
     __syncthreads();
-    // row max of score * scaling: 16 lanes per row, wave w rows 4w .. 4w+3
+    const int nrows = imax - i0 + 1;  // valid query rows of the block
+    // per row (16 lanes, wave w rows 4w .. 4w+3): score = S1 + S2[t-1-i+j] in place in s1, the row max of
+    // score * scaling, then exp_poly(score * scaling - max) in place
     {
         const int r = wave * 4 + (lane >> 4), l16 = lane & 15;
         float m = -INFINITY;
-        if (r < nrows)
-            for (int j = l16; j < t; j += 16) m = fmaxf(m, s1[r * s1w + j] * scaling);
+        if (r < nrows) {
+            const float *s2r = s2 + r * s2w + (t - 1 - (i0 + r) - pb0);
+            for (int j = l16; j < t; j += 16) {
+                const float sc = s1[r * s1w + j] + s2r[j];
+                s1[r * s1w + j] = sc;
+                m = fmaxf(m, sc * scaling);
+            }
+        }
 #pragma unroll
         for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        if (l16 == 0) rowv[r] = m;
-    }
-    __syncthreads();
-    for (int e = tid; e < 16 * t; e += 256) {
-        const int r = e / t, j = e % t;
-        if (r < nrows) s1[r * s1w + j] = exp_poly(s1[r * s1w + j] * scaling - rowv[r]);
+        if (r < nrows)
+            for (int j = l16; j < t; j += 16) s1[r * s1w + j] = exp_poly(s1[r * s1w + j] * scaling - m);
     }
     __syncthreads();
     // row sums in the reference's order: lane 4r + l keeps the running sum of columns j = 4q + l
@@ -256,8 +277,10 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
         const int r = lane >> 2, l = lane & 3;
         const int t4 = t / 4 * 4;
         float acc = 0.0f;
-        if (r < nrows)
+        if (r < nrows) {
+#pragma unroll 8
             for (int j = l; j < t4; j += 4) acc += s1[r * s1w + j];
+        }
         const int base = lane & ~3;
         const float l0 = __shfl(acc, base, 64), l1 = __shfl(acc, base + 1, 64), l2 = __shfl(acc, base + 2, 64),
                     l3 = __shfl(acc, base + 3, 64);
@@ -283,18 +306,35 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
     }
     __syncthreads();
     // context: channel blocks 2*wave, 2*wave+1; K over tv in 64-steps; A = pq rows from LDS, B = vT rows
+    // (the vT loads of kPF K steps of both blocks are issued before their MFMAs)
     float val[2][4];
+    v4i pacc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+    {
+        const int8_t *vr0 = W.vq + ((int64_t)h * kDh + 2 * wave * 16 + arow) * D.tv + 16 * aq;
+        const int8_t *vr1 = vr0 + (int64_t)16 * D.tv;
+        const int8_t *pr = pq + arow * D.tv + 16 * aq;
+        for (int k0 = 0; k0 < D.tv; k0 += 64 * kPF) {
+            v4i b[2][kPF];
+#pragma unroll
+            for (int p = 0; p < kPF; p++) {
+                const int kk = min(k0 + 64 * p, D.tv - 64);
+                b[0][p] = *(const v4i *)(vr0 + kk);
+                b[1][p] = *(const v4i *)(vr1 + kk);
+            }
+#pragma unroll
+            for (int p = 0; p < kPF; p++) {
+                if (k0 + 64 * p < D.tv) {
+                    const v4i a = *(const v4i *)(pr + k0 + 64 * p);
+                    pacc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[0][p], pacc[0], 0, 0, 0);
+                    pacc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[1][p], pacc[1], 0, 0, 0);
+                }
+            }
+        }
+    }
 #pragma unroll
     for (int cbi = 0; cbi < 2; cbi++) {
         const int cb = 2 * wave + cbi;
-        v4i acc = {0, 0, 0, 0};
-        const int8_t *vr = W.vq + ((int64_t)h * kDh + cb * 16 + arow) * D.tv + 16 * aq;
-        const int8_t *pr = pq + arow * D.tv + 16 * aq;
-        for (int k0 = 0; k0 < D.tv; k0 += 64) {
-            const v4i a = *(const v4i *)(pr + k0);
-            const v4i b = *(const v4i *)(vr + k0);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
-        }
+        const v4i acc = pacc[cbi];
         const int c = cb * 16 + dcol;
         const float vsv = W.vs[h * kDh + c];
 #pragma unroll
