@@ -338,3 +338,26 @@ def test_attention_core_quantize_equals_oracle(dev, orc, t, heads):
     _bits_equal(st[:, :t].T.copy(), ws, f"scales t={t}")
     np.testing.assert_array_equal(gt[:, :t].T, wg, err_msg=f"gsum t={t}")
     assert not st[:, t:].any() and not gt[:, t:].any(), f"pad tokens not zero t={t}"
+
+
+def test_encoder_from_model_directory(dev, orc, tmp_path):
+    """An encoder loaded from a model directory (thrush-ternary-v2 files, HF tensor names; voxrt_amd.model) equals
+    the oracle encoder on the same file's parameters: subsampling and two layers from features, bit for bit."""
+    from modeldir import synth_model, write_model_dir
+    from voxrt_amd import encoder as E
+    from voxrt_amd import model as M
+
+    layers, sp = synth_model(d=1024, heads=8, ff=4096, n_layers=2, n_mels=128, c=256)
+    path = write_model_dir(str(tmp_path / "model"), layers, sp, d=1024, heads=8, ff=4096, n_mels=128, c=256)
+    m = M.ModelFile(path)
+    assert m.validate() == []
+    enc = M.load_encoder(m)
+    feats = _x(77, 203, 128)
+    got = enc.forward_feats(_t(feats, dev)).cpu().numpy()
+    enc.free()
+    x = orc.subsampling(feats, M.subsampling_params(m))
+    t = x.shape[0]
+    pos = orc.rel_pos_table(t, 1024)
+    for i in range(2):
+        x = orc.conformer_layer(x, pos, _oracle_layer(orc, M.layer_params(m, i)), heads=8)
+    _bits_equal(got, x, "encoder from a model directory")
