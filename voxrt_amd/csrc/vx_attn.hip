@@ -12,8 +12,9 @@
 //   multiplied by 1/sum; ctx[i][h*dh + c] = fma((float)(p_i . v_c), s_p[i] * s_v[c], 0).
 //
 // Kernels:
-//   attn_rows_kernel  : one wavefront per 128-wide row: q+bias_u, q+bias_v, k (tokens), relative rows; quantize.
-//   attn_vt_kernel    : one wavefront per (head, channel): the column of v over the tokens, quantized.
+//   attn_prep_kernel  : the row items (one wavefront per 128-wide row: q+bias_u, q+bias_v, k (tokens), relative
+//                       rows; quantize) and the vT items (one wavefront per (head, channel): the column of v over
+//                       the tokens, quantized) in one launch.
 //   attn_core_kernel  : one workgroup per (head, 16 query rows). Content scores for all keys and the position band
 //                       [t-1-i_max, 2t-2-i0] through v_mfma_i32_16x16x64_i8 into LDS; softmax in LDS (the four
 //                       running sums per row on four lanes, so the order is the reference's); the probabilities
@@ -69,11 +70,10 @@ __device__ inline float quant128(float a0, float a1, int lane, int8_t *dst) {
 }
 
 // Work items: [0, nseg*h*tp) query/key rows (segment-major, then head-major), then h*rp relative rows (shared).
-__global__ __launch_bounds__(256) void attn_rows_kernel(const float *__restrict__ qkv, const float *__restrict__ rel_k,
-                                                       const float *__restrict__ bias_u,
-                                                       const float *__restrict__ bias_v, AttnDims D, AttnWs W) {
+__device__ inline void attn_rows_item(int item, const float *__restrict__ qkv, const float *__restrict__ rel_k,
+                                      const float *__restrict__ bias_u, const float *__restrict__ bias_v,
+                                      const AttnDims &D, const AttnWs &W) {
     const int lane = threadIdx.x & 63;
-    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int d3 = 3 * D.d;
     if (item < D.nseg * D.h * D.tp) {
         const int seg = item / (D.h * D.tp), hi = item % (D.h * D.tp);
@@ -117,9 +117,8 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(const float *__restrict_
 }
 
 // One wavefront per (segment, head, channel): vT row = v[i][h*dh + c] for i < t, zero to tv; one group.
-__global__ __launch_bounds__(256) void attn_vt_kernel(const float *__restrict__ qkv, AttnDims D, AttnWs W) {
+__device__ inline void attn_vt_item(int item, const float *__restrict__ qkv, const AttnDims &D, const AttnWs &W) {
     const int lane = threadIdx.x & 63;
-    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (item >= D.nseg * D.h * kDh) return;
     const int seg = item / (D.h * kDh), hc = item % (D.h * kDh);
     const int h = hc / kDh, c = hc % kDh;
@@ -133,6 +132,19 @@ __global__ __launch_bounds__(256) void attn_vt_kernel(const float *__restrict__ 
     int8_t *dst = W.vq + ((int64_t)item) * D.tv;
     for (int i = lane; i < D.tv; i += 64) dst[i] = i < D.t ? q_code(col[i * ld], inv) : (int8_t)0;
     if (lane == 0) W.vs[item] = s;
+}
+
+// The per-row quantizations and the vT rows in one launch: the first `rows_blocks` workgroups take the row items,
+// the others the vT items (four wavefronts, one item each).
+__global__ __launch_bounds__(256) void attn_prep_kernel(const float *__restrict__ qkv, const float *__restrict__ rel_k,
+                                                       const float *__restrict__ bias_u,
+                                                       const float *__restrict__ bias_v, AttnDims D, AttnWs W,
+                                                       int rows_blocks) {
+    const int wv = threadIdx.x >> 6;
+    if ((int)blockIdx.x < rows_blocks)
+        attn_rows_item((int)blockIdx.x * 4 + wv, qkv, rel_k, bias_u, bias_v, D, W);
+    else
+        attn_vt_item(((int)blockIdx.x - rows_blocks) * 4 + wv, qkv, D, W);
 }
 
 // LDS plan of attn_core_kernel (bytes): s1 [16][s1w] f32, s2 [16][s2w] f32, pq [16][tv] int8, row stats.
@@ -451,10 +463,10 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
     W.rs = (float *)take(rrows * 4);
     W.vs = (float *)take((size_t)(nseg * h) * kDh * 4);
     const int items = (int)(rows + rrows);
-    attn_rows_kernel<<<(unsigned)((items + 3) / 4), 256, 0, st>>>(qkv, rel_k, bias_u, bias_v, D, W);
-    hip_check(hipGetLastError(), "attention rows kernel launch");
-    attn_vt_kernel<<<(unsigned)((nseg * h * kDh + 3) / 4), 256, 0, st>>>(qkv, D, W);
-    hip_check(hipGetLastError(), "attention vT kernel launch");
+    const int rows_blocks = (items + 3) / 4, vt_blocks = (int)((nseg * h * kDh + 3) / 4);
+    attn_prep_kernel<<<(unsigned)(rows_blocks + vt_blocks), 256, 0, st>>>(qkv, rel_k, bias_u, bias_v, D, W,
+                                                                         rows_blocks);
+    hip_check(hipGetLastError(), "attention rows / vT kernel launch");
     const size_t lds = core_lds_bytes((int)t);
     static bool lds_raised = false;
     if (!lds_raised) {

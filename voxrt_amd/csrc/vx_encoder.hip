@@ -37,6 +37,9 @@ void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const fl
 void gemm_quant(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y_tmp,
                 const float *bias, int ep, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st);
 void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y, hipStream_t stream);
+void layer_norm_quantize_ln(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y,
+                            int64_t group, const float *g2, const float *b2, int8_t *q, float *scales_t,
+                            int32_t *gsum_t, hipStream_t stream);
 void glu_dwconv_silu_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
                          const float *bias, float *out, hipStream_t st);
 void glu_dwconv_silu_quant_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
@@ -209,7 +212,11 @@ void run_layers(vx_encoder *e, EncWs &w, hipStream_t st) {
                         st);
         };
         auto ffn = [&](int norm, int w1, int w2) {
-            lnq(norm);
+            if (norm == 0 && li > 0) {
+                // this layer's norm_feed_forward1 -> quantize ran with the previous layer's norm_out
+            } else {
+                lnq(norm);
+            }
             // h = silu(W1 q) quantized for W2 in one call (up to 1024 rows the GEMM quantizes in its epilogue and
             // h never reaches memory; above, hbuf carries it)
             gemm_quant(&L.lin[w1]->m, w.a.q.as<int8_t>(), w.a.s.as<float>(), w.a.g.as<int32_t>(), t, w.hbuf.as<float>(),
@@ -246,7 +253,14 @@ void run_layers(vx_encoder *e, EncWs &w, hipStream_t st) {
         }
         gemm_full(L.lin[6], w.a, t, x, VX_EP_ADD_SCALED, 1.0f, st);
         ffn(3, 7, 8);
-        layer_norm(x, t, d, L.ln_g[4].as<float>(), L.ln_b[4].as<float>(), xn, st);
+        if (li + 1 < e->layers.size()) {  // norm_out, then the next layer's first LayerNorm -> quantize
+            EncLayer &Ln = *e->layers[li + 1];
+            layer_norm_quantize_ln(x, t, d, L.ln_g[4].as<float>(), L.ln_b[4].as<float>(), xn, G,
+                                   Ln.ln_g[0].as<float>(), Ln.ln_b[0].as<float>(), w.a.q.as<int8_t>(),
+                                   w.a.s.as<float>(), w.a.g.as<int32_t>(), st);
+        } else {
+            layer_norm(x, t, d, L.ln_g[4].as<float>(), L.ln_b[4].as<float>(), xn, st);
+        }
     }
 }
 

@@ -143,12 +143,17 @@ __global__ __launch_bounds__(256) void quantize_fast_kernel(const float *__restr
 // Row-resident path: inp = NC * 1024 (NC <= 4), one wavefront per token, the row loaded once into registers
 // (16 consecutive floats per lane per 1024-column chunk). With LN the row is also staged in the wavefront's LDS
 // slot, where lanes 0-7 run the reference-order statistics. MODE 0 quantizes, MODE 1 writes the LayerNorm row as
-// float32 (y). Waves of pad tokens [n, np) only write zero scales and code sums, so no pad launch is needed.
+// float32 (y), MODE 2 writes that row to y and then quantizes its LayerNorm with (lg2, lb2): a layer's norm_out
+// followed by the next layer's first LayerNorm->quantize in one pass. Waves of pad tokens [n, np) only write zero
+// scales and code sums, so no pad launch is needed.
 template <int L, int NC, bool LN, int MODE>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict__ x, int n, int np, int group,
                                                         int8_t *__restrict__ q, float *__restrict__ st,
                                                         int32_t *__restrict__ gt, const float *__restrict__ lg,
-                                                        const float *__restrict__ lb, float *__restrict__ y) {
+                                                        const float *__restrict__ lb, float *__restrict__ y,
+                                                        const float *__restrict__ lg2,
+                                                        const float *__restrict__ lb2) {
+    static_assert(MODE != 2 || LN, "MODE 2 is two LayerNorms");
     constexpr int inp = NC * 1024;
     __shared__ __attribute__((aligned(16))) float srow[LN ? 4 : 1][LN ? inp : 4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
     if (t >= np) return;
     const int ng = inp / group;
     if (t >= n) {
-        if (MODE == 0)
+        if (MODE != 1)
             for (int g = lane; g < ng; g += 64) {
                 st[(int64_t)g * np + t] = 0.0f;
                 gt[(int64_t)g * np + t] = 0;
@@ -165,6 +170,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
     }
     const float *xr = x + (int64_t)t * inp;
     float4 lgv[LN ? NC : 1][4], lbv[LN ? NC : 1][4];  // gamma / beta quads, fetched with the row
+    float4 lgv2[MODE == 2 ? NC : 1][4], lbv2[MODE == 2 ? NC : 1][4];
     if constexpr (LN) {
 #pragma unroll
         for (int c = 0; c < NC; c++)
@@ -172,6 +178,10 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
             for (int i = 0; i < 4; i++) {
                 lgv[c][i] = ((const float4 *)(lg + c * 1024 + lane * 16))[i];
                 lbv[c][i] = ((const float4 *)(lb + c * 1024 + lane * 16))[i];
+                if constexpr (MODE == 2) {
+                    lgv2[c][i] = ((const float4 *)(lg2 + c * 1024 + lane * 16))[i];
+                    lbv2[c][i] = ((const float4 *)(lb2 + c * 1024 + lane * 16))[i];
+                }
             }
     }
     float v[NC][16];
@@ -187,7 +197,8 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
             v[c][4 * i + 3] = f.w;
         }
     }
-    if constexpr (LN) {
+    // LayerNorm of the row in v, in place: statistics in the reference's order over the row staged in LDS
+    auto ln_pass = [&](const float4 (&G)[LN ? NC : 1][4], const float4 (&B)[LN ? NC : 1][4]) __attribute__((always_inline)) {
         // the row transposed by column residue: T[j][k] = x[8k + j], so that the running sum of residue j (the
         // reference's lane j of row_mean_var_portable) walks contiguous memory
         constexpr int KL = inp / 8;
@@ -242,15 +253,16 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
         for (int c = 0; c < NC; c++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float4 g4 = lgv[c][i], b4 = lbv[c][i];
+                const float4 g4 = G[c][i], b4 = B[c][i];
                 v[c][4 * i] = ln_apply(v[c][4 * i], mean, linv, g4.x, b4.x);
                 v[c][4 * i + 1] = ln_apply(v[c][4 * i + 1], mean, linv, g4.y, b4.y);
                 v[c][4 * i + 2] = ln_apply(v[c][4 * i + 2], mean, linv, g4.z, b4.z);
                 v[c][4 * i + 3] = ln_apply(v[c][4 * i + 3], mean, linv, g4.w, b4.w);
             }
         }
-    }
-    if constexpr (MODE == 1) {
+    };
+    if constexpr (LN) ln_pass(lgv, lbv);
+    if constexpr (MODE != 0) {
         float *yr = y + (int64_t)t * inp;
 #pragma unroll
         for (int c = 0; c < NC; c++)
@@ -258,8 +270,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
             for (int i = 0; i < 4; i++)
                 *(float4 *)(yr + c * 1024 + lane * 16 + 4 * i) =
                     make_float4(v[c][4 * i], v[c][4 * i + 1], v[c][4 * i + 2], v[c][4 * i + 3]);
-        return;
+        if constexpr (MODE == 1) return;
     }
+    if constexpr (MODE == 2) ln_pass(lgv2, lbv2);
     // groups of L lanes (group = 16 L columns) or whole chunks (L = 64, group = 1024 * k)
     int8_t *qr = q + (int64_t)t * inp;
     constexpr int CPG = 1;  // chunks per group when L == 64 is handled below
@@ -408,7 +421,7 @@ void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const fl
         const unsigned blk = (unsigned)((np + 3) / 4);
 #define VX_QR(LL, NC)                                                                                                \
     (ln ? quant_rows_kernel<LL, NC, true, 0> : quant_rows_kernel<LL, NC, false, 0>)<<<blk, 256, 0, stream>>>(       \
-        x, ni, np, gi, q, scales_t, gsum_t, g, b, nullptr)
+        x, ni, np, gi, q, scales_t, gsum_t, g, b, nullptr, nullptr, nullptr)
 #define VX_QR_NC(LL)                                                                                                 \
     switch (nc) {                                                                                                    \
         case 1: VX_QR(LL, 1); break;                                                                                 \
@@ -479,16 +492,56 @@ void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const floa
         const unsigned blk = (unsigned)((n + 3) / 4);
         const int ni = (int)n;
         switch (d / 1024) {
-            case 1: quant_rows_kernel<4, 1, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y); break;
-            case 2: quant_rows_kernel<4, 2, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y); break;
-            case 3: quant_rows_kernel<4, 3, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y); break;
-            default: quant_rows_kernel<4, 4, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y); break;
+            case 1: quant_rows_kernel<4, 1, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y, nullptr, nullptr); break;
+            case 2: quant_rows_kernel<4, 2, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y, nullptr, nullptr); break;
+            case 3: quant_rows_kernel<4, 3, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y, nullptr, nullptr); break;
+            default: quant_rows_kernel<4, 4, true, 1><<<blk, 256, 0, stream>>>(x, ni, ni, 64, nullptr, nullptr, nullptr, g, b, y, nullptr, nullptr); break;
         }
         hip_check(hipGetLastError(), "layer_norm kernel launch");
         return;
     }
     layer_norm_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(x, (int)n, (int)d, g, b, y);
     hip_check(hipGetLastError(), "layer_norm kernel launch");
+}
+
+// A layer's norm_out (tensor.rs:700-719, encoder.rs:755) into y, then the next layer's first prepare_normed
+// (norm_feed_forward1 -> quantize, ternary_linear.rs:132-155) of y, in one pass over each row: bit for bit as
+// layer_norm followed by quantize_ln, with one launch and one read of the row fewer.
+void layer_norm_quantize_ln(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y,
+                            int64_t group, const float *g2, const float *b2, int8_t *q, float *scales_t,
+                            int32_t *gsum_t, hipStream_t stream) {
+    require(x && g && b && y && g2 && b2 && q && scales_t && gsum_t, "LayerNorm -> quantize: NULL pointer");
+    require(n >= 0 && d > 0 && group > 0 && d % group == 0 && n * d < (1ll << 31), "bad LayerNorm shape");
+    if (n == 0) return;
+    auto al16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool pow2 = group >= 64 && group <= 1024 && (group & (group - 1)) == 0;
+    if (d % 1024 == 0 && d <= 4096 && pow2 && al16(x) && al16(y) && al16(g) && al16(b) && al16(g2) && al16(b2) &&
+        al16(q)) {
+        const int ni = (int)n, np = (int)((n + 15) / 16 * 16), gi = (int)group;
+        const unsigned blk = (unsigned)((np + 3) / 4);
+#define VX_LQ(LL, NC)                                                                                                \
+    quant_rows_kernel<LL, NC, true, 2><<<blk, 256, 0, stream>>>(x, ni, np, gi, q, scales_t, gsum_t, g, b, y, g2, b2)
+#define VX_LQ_NC(LL)                                                                                                 \
+    switch (d / 1024) {                                                                                              \
+        case 1: VX_LQ(LL, 1); break;                                                                                 \
+        case 2: VX_LQ(LL, 2); break;                                                                                 \
+        case 3: VX_LQ(LL, 3); break;                                                                                 \
+        default: VX_LQ(LL, 4); break;                                                                                \
+    }
+        switch (group) {
+            case 64: VX_LQ_NC(4); break;
+            case 128: VX_LQ_NC(8); break;
+            case 256: VX_LQ_NC(16); break;
+            case 512: VX_LQ_NC(32); break;
+            default: VX_LQ_NC(64); break;
+        }
+#undef VX_LQ_NC
+#undef VX_LQ
+        hip_check(hipGetLastError(), "LayerNorm -> quantize kernel launch");
+        return;
+    }
+    layer_norm(x, n, d, g, b, y, stream);
+    quantize_ln(y, n, d, group, g2, b2, q, scales_t, gsum_t, stream);
 }
 
 }  // namespace vx
