@@ -37,6 +37,7 @@ __host__ __device__ inline int up64(int x) { return (x + 63) / 64 * 64; }
 struct AttnDims {
     int t, d, h, np, tp, rp, tv;
     int nseg = 1;  // segments of t frames each: qkv and ctx are [nseg][t][...], the relative rows are shared
+    int rel_ld = 0;  // row pitch (floats) of rel_k: d, or wider when rel_k is one layer's block of a stacked output
     __host__ __device__ AttnDims(int t_, int d_, int h_) : t(t_), d(d_), h(h_) {
         np = 2 * t - 1;
         tp = up16(t);       // token rows (queries, keys)
@@ -108,7 +109,7 @@ __device__ inline void attn_rows_item(int item, const float *__restrict__ qkv, c
     const int h = r / D.rp, p = r % D.rp;
     float a0 = 0.0f, a1 = 0.0f;
     if (p < D.np) {
-        const float2 v = *(const float2 *)(rel_k + (int64_t)p * D.d + h * kDh + 2 * lane);
+        const float2 v = *(const float2 *)(rel_k + (int64_t)p * D.rel_ld + h * kDh + 2 * lane);
         a0 = v.x;
         a1 = v.y;
     }
@@ -435,7 +436,7 @@ size_t attn_ws_bytes(int64_t t, int64_t d, int64_t h) { return attn_ws_bytes_seg
 // groups (one per head): q int8 [nseg * t][d], scales_t and gsum_t [h][npad(nseg * t)].
 void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
                         const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
-                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t) {
+                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t, int64_t rel_ld) {
     const bool qout = q != nullptr;
     require(qkv && rel_k && bias_u && bias_v && ws && (ctx || qout) && (!qout || (scales_t && gsum_t)),
             "attention: NULL pointer");
@@ -444,6 +445,8 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
     require(nseg >= 1 && nseg <= 65535 && nseg * t * 3 * d < (1ll << 31), "attention: 1 <= segments, size < 2^31");
     AttnDims D((int)t, (int)d, (int)h);
     D.nseg = (int)nseg;
+    require(rel_ld >= d && (2 * t - 1) * rel_ld < (1ll << 31), "attention: bad rel_k row pitch");
+    D.rel_ld = (int)rel_ld;
     uint8_t *p = (uint8_t *)ws;
     auto take = [&](size_t n) {
         uint8_t *r = p;
@@ -490,7 +493,7 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
 // ctx [t][d] from qkv [t][3d] (q | k | v) and rel_k [2t-1][d]; ws is attn_ws_bytes(t, d, h) device bytes.
 void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h, const float *bias_u,
                     const float *bias_v, float scaling, void *ws, float *ctx, hipStream_t st) {
-    attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, ws, ctx, st, nullptr, nullptr, nullptr);
+    attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, ws, ctx, st, nullptr, nullptr, nullptr, d);
 }
 
 }  // namespace vx

@@ -56,7 +56,7 @@ void rel_pos_table(int64_t t, int64_t d, float *out);
 size_t attn_ws_bytes_seg(int64_t t, int64_t d, int64_t h, int64_t nseg);
 void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
                         const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
-                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t);
+                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t, int64_t rel_ld);
 
 namespace {
 
@@ -108,6 +108,8 @@ struct QBuf {  // one quantized activation block: q [n][inp], scales_t / gsum_t 
 
 struct EncLayer {
     vx_tmat *lin[9] = {};
+    std::vector<uint8_t> pos_q;   // relative_k_proj packed rows and f16 scales (host), for the stacked projection
+    std::vector<uint16_t> pos_s;
     DevBuf ln_g[5], ln_b[5], bias_u, bias_v, dw_t, dw_bias;
     bool set = false;
     ~EncLayer() {
@@ -132,6 +134,13 @@ struct EncWs {  // everything one forward of nseg segments of t frames touches
 struct vx_encoder {
     vx_encoder_config cfg;
     std::vector<std::unique_ptr<vx::EncLayer>> layers;
+    // the relative_k_proj matrices of all layers stacked along the output rows (layer l: rows [l*d, (l+1)*d)),
+    // built from the layers' host copies before the first forward after a change
+    vx_tmat *pos_all = nullptr;
+    bool pos_dirty = true;
+    ~vx_encoder() {
+        if (pos_all) vx::free_tmat(pos_all);
+    }
     vx::DevBuf sub_w[8];
     bool sub_set = false;
     bool graphs = true;
@@ -169,7 +178,7 @@ EncWs &workspace(vx_encoder *e, int64_t t, int64_t nseg) {
     for (auto &x : w->x) x = DevBuf((size_t)(n * c.d) * f4);
     w->hbuf = DevBuf((size_t)(n * c.ff) * f4);
     w->qkv = DevBuf((size_t)(n * 3 * c.d) * f4);
-    w->rel_k = DevBuf((size_t)(w->np * c.d) * f4);
+    w->rel_k = DevBuf((size_t)(w->np * c.n_layers * c.d) * f4);  // [np][n_layers * d]: every layer's projection
     w->ctx = DevBuf((size_t)(n * c.d) * f4);
     w->g2 = DevBuf((size_t)(n * 2 * c.d) * f4);
     w->hb = DevBuf((size_t)(n * c.d) * f4);
@@ -200,6 +209,10 @@ void run_layers(vx_encoder *e, EncWs &w, hipStream_t st) {
     const vx_encoder_config &c = e->cfg;
     const int64_t t = w.nseg * w.t, d = c.d, G = c.group;
     const float scaling = 1.0f / std::sqrt((float)(d / c.heads));
+    // relative_k_proj of the position table for all layers in one GEMM (it depends on t and the weights only):
+    // rel_k [np][n_layers * d], layer l's block at columns [l*d, (l+1)*d)
+    const int64_t rel_ld = (int64_t)e->layers.size() * d;
+    gemm_full(e->pos_all, w.posq, w.np, w.rel_k.as<float>(), VX_EP_STORE, 0.0f, st);
     for (size_t li = 0; li < e->layers.size(); li++) {
         EncLayer &L = *e->layers[li];
         float *x = w.x[li % 2].as<float>(), *xn = w.x[(li + 1) % 2].as<float>();
@@ -227,15 +240,14 @@ void run_layers(vx_encoder *e, EncWs &w, hipStream_t st) {
         // attention
         lnq(1);
         gemm_full(L.lin[2], w.a, t, w.qkv.as<float>(), VX_EP_STORE, 0.0f, st);
-        gemm_full(L.lin[4], w.posq, w.np, w.rel_k.as<float>(), VX_EP_STORE, 0.0f, st);
         if (G == 128) {  // a head's 128 channels are one group: the core writes the o-projection's activations
-            attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>(), w.nseg, w.t, d, c.heads, L.bias_u.as<float>(),
-                               L.bias_v.as<float>(), scaling, w.attn.p, nullptr, st, w.a.q.as<int8_t>(),
-                               w.a.s.as<float>(), w.a.g.as<int32_t>());
+            attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>() + li * d, w.nseg, w.t, d, c.heads,
+                               L.bias_u.as<float>(), L.bias_v.as<float>(), scaling, w.attn.p, nullptr, st,
+                               w.a.q.as<int8_t>(), w.a.s.as<float>(), w.a.g.as<int32_t>(), rel_ld);
         } else {
-            attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>(), w.nseg, w.t, d, c.heads, L.bias_u.as<float>(),
-                               L.bias_v.as<float>(), scaling, w.attn.p, w.ctx.as<float>(), st, nullptr, nullptr,
-                               nullptr);
+            attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>() + li * d, w.nseg, w.t, d, c.heads,
+                               L.bias_u.as<float>(), L.bias_v.as<float>(), scaling, w.attn.p, w.ctx.as<float>(), st,
+                               nullptr, nullptr, nullptr, rel_ld);
             quant(w.ctx.as<float>(), d, w.a);
         }
         gemm_full(L.lin[3], w.a, t, x, VX_EP_ADD_SCALED, 1.0f, st);
@@ -264,9 +276,22 @@ void run_layers(vx_encoder *e, EncWs &w, hipStream_t st) {
     }
 }
 
-void check_ready(const vx_encoder *e) {
+void check_ready(vx_encoder *e) {
     for (size_t i = 0; i < e->layers.size(); i++)
         if (!e->layers[i]->set) throw Error(VX_ERR_INVALID, "encoder layer " + std::to_string(i) + " has no weights");
+    if (e->pos_dirty) {  // stack the layers' relative_k_proj matrices (TernaryLinear::load_stacked's row order)
+        const vx_encoder_config &c = e->cfg;
+        std::vector<uint8_t> q;
+        std::vector<uint16_t> s;
+        for (auto &L : e->layers) {
+            q.insert(q.end(), L->pos_q.begin(), L->pos_q.end());
+            s.insert(s.end(), L->pos_s.begin(), L->pos_s.end());
+        }
+        vx_tmat *all = upload_packed(q.data(), s.data(), true, (int64_t)e->layers.size() * c.d, c.d, c.group);
+        if (e->pos_all) free_tmat(e->pos_all);
+        e->pos_all = all;
+        e->pos_dirty = false;
+    }
 }
 
 // x (device [nseg][t][d]) -> the encoder output (device [nseg][t][d]), both caller buffers (they may alias).
@@ -359,6 +384,10 @@ void encoder_set_layer(vx_encoder *e, int64_t li, const vx_layer_params *p) {
     fold_bn(p->dw, p->bn_gamma, p->bn_beta, p->bn_mean, p->bn_var, c.d, c.kconv, wt.data(), bias.data());
     L->dw_t = upload(wt.data(), wt.size() * sizeof(float));
     L->dw_bias = upload(bias.data(), dv);
+    const size_t pq = (size_t)(c.d * ((c.d + 4) / 5)), ps = (size_t)(c.d * (c.d / c.group));
+    L->pos_q.assign(p->qweight[4], p->qweight[4] + pq);
+    L->pos_s.assign(p->scales_f16[4], p->scales_f16[4] + ps);
+    e->pos_dirty = true;
     L->set = true;
     e->layers[(size_t)li] = std::move(L);
     for (auto &kv : e->ws)
