@@ -236,25 +236,28 @@ def encoder_rtfx(torch, synth, enc, dev, reps=5):
     return out
 
 
-def clip_batch_tops(torch, vx, synth, dev, params, reps=3):
+def clip_batch_tops(torch, vx, synth, dev, params, reps=3, group=None):
     """64 short clips (25 + lcg % 164 frames each, 2-15 s) concatenated to M rows of per-token int8 activations
-    (group = K) through the linear layers of all 24 layers (ff1 up/down, q|k|v, out, pw1, pw2, ff2 up/down; the
-    position projection depends on each clip's length and is left out), per-output-channel scales. Returns the
-    aggregate TOPS of one pass over the 192 GEMMs."""
+    through the linear layers of all 24 layers (ff1 up/down, q|k|v, out, pw1, pw2, ff2 up/down; the position
+    projection depends on each clip's length and is left out). group None: one group (per-output-channel scales,
+    G = K); 128: the model's 128-column groups. Returns the aggregate TOPS of one pass over the 192 GEMMs."""
     lens = 25 + synth.Lcg(synth.workload_seed(2, 0)).take(64) % 164
     m = int(lens.sum())
     names = ("ff1_w1", "ff1_w2", "qkv", "o", "pw1", "pw2", "ff2_w1", "ff2_w2")
     acts = {}
     for k in (1024, 4096):
         x = torch.from_numpy(synth.synth_normal(synth.workload_seed(2, k >> 10), m * k).reshape(m, k)).to(dev)
-        acts[k] = vx.QuantAct.quantize(x, k)
+        acts[k] = vx.QuantAct.quantize(x, group or k)
         del x
     work, ops, ys = [], 0.0, {}
     for p in params:
         for n in names:
             q, s16 = p["linears"][n]
             out, inp = s16.shape[0], s16.shape[1] * 128
-            w = vx.TernaryMatrix.from_packed(q, np.ascontiguousarray(s16[:, :1]), out, inp, inp)
+            if group:
+                w = vx.TernaryMatrix.from_packed(q, s16, out, inp, group)
+            else:
+                w = vx.TernaryMatrix.from_packed(q, np.ascontiguousarray(s16[:, :1]), out, inp, inp)
             if out not in ys:  # one output buffer per width: the GEMMs run one after another
                 ys[out] = torch.empty((m, out), dtype=torch.float32, device=dev)
             work.append((w, acts[inp], ys[out]))
@@ -276,8 +279,76 @@ def clip_batch_tops(torch, vx, synth, dev, params, reps=3):
     sec = e0.elapsed_time(e1) * 1e-3 / reps
     del graph, work, acts, ys
     torch.cuda.empty_cache()
-    return {"clips": 64, "rows": m, "gemms": 192, "ms": round(sec * 1e3, 3), "tops": round(ops / sec / 1e12, 1),
+    return {"clips": 64, "rows": m, "gemms": 192, "group": group or "K", "ms": round(sec * 1e3, 3),
+            "tops": round(ops / sec / 1e12, 1),
             "pct_int8_peak": round(100 * ops / sec / 1e12 / PEAK_INT8_TOPS, 1)}
+
+
+def cpu_vnni_single_core(synth):
+    """The reference's per-core CPU GEMM protocol (tests/x86_bench.rs:31-72): FF shapes 4096x1024 and 1024x4096,
+    n = 376 tokens, trits lcg % 3 - 1 and x = (lcg % 2001)/100 - 10 from seed 1, f16 scales 0.02, group 128, a
+    256-row slice through the VNNI range kernel on one thread, best of 5; GMAC/s per core, as bench/README.md:122-123
+    quotes (337-359 on a Zen 5 core)."""
+    from oracle import oracle
+
+    if not oracle.lib().or_have_vnni():
+        return None
+    rng = synth.Lcg(1)
+    out_rates = {}
+    for out, inp in ((4096, 1024), (1024, 4096)):
+        n, rows = 376, 256
+        trits = (rng.take(out * inp) % 3).astype(np.int8).reshape(out, inp) - 1
+        ws = np.full((out, inp // 128), np.float32(np.float16(0.02)), np.float32)
+        xf = ((rng.take(n * inp) % 2001).astype(np.float32) / np.float32(100.0) - np.float32(10.0)).reshape(n, inp)
+        q, xs, gsum = oracle.quantize(xf, 128)
+        wq, sq = oracle.quad16_pack(trits.astype(np.int8), ws, 128)
+        y = np.zeros((n, out), np.float32)
+        best = float("inf")
+        for _ in range(5):
+            t0 = time.perf_counter()
+            oracle.gemm_vnni_range(wq, sq, out, inp, 128, q, xs, gsum, y, 0, rows, 0, n)
+            best = min(best, time.perf_counter() - t0)
+        out_rates[f"{out}x{inp}"] = round(rows * inp * n / best / 1e9, 1)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"gmac_per_s_per_core": out_rates, "threads": 1, "cpu": model, "logical_cpus": os.cpu_count(),
+            "protocol": "x86_bench.rs: n=376, 256-row slice, best of 5, AVX-512 VNNI restatement"}
+
+
+def attention_us(torch, dev, reps=10):
+    """The int8 attention core of one layer alone (8 heads, head_dim 128; q|k|v and the relative rows N(0,1)):
+    microseconds per call at T = 338 and 750, and the MAC rate over its 3072*T^2 MACs (Q.K, Q.R band, P.V)."""
+    from voxrt_amd import encoder as E
+
+    out = {}
+    for t in (338, 750):
+        r = np.random.default_rng(t)
+        qkv = torch.from_numpy(r.standard_normal((t, 3072)).astype(np.float32)).to(dev)
+        rel = torch.from_numpy(r.standard_normal((2 * t - 1, 1024)).astype(np.float32)).to(dev)
+        bu = torch.from_numpy((0.1 * r.standard_normal((8, 128))).astype(np.float32)).to(dev)
+        bv = torch.from_numpy((0.1 * r.standard_normal((8, 128))).astype(np.float32)).to(dev)
+        ctx = torch.empty((t, 1024), dtype=torch.float32, device=dev)
+        ws = torch.empty(max(E.attention_ws_bytes(t, 1024, 8), 1), dtype=torch.uint8, device=dev)
+        graph = capture(torch, lambda: E.attention_core(qkv, rel, 8, bu, bv, ctx=ctx, ws=ws), reps)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (3 * reps)
+        del graph
+        out[f"t{t}"] = {"us": round(us, 2), "gmac_per_s": round(3072 * t * t / us * 1e-3, 1)}
+    return out
 
 
 def cpu_encoder_rtfx(params, sp, synth, budget_s=30.0):
@@ -421,12 +492,16 @@ def main():
                                "hbm_gbs": round(g.bytes / s / 1e9, 0)}
         del extra
     cpu = None if args.no_cpu else cpu_baseline(gemms)
+    if not args.no_cpu and not args.no_details:
+        details["cpu_vnni_single_core"] = cpu_vnni_single_core(synth)
     if not args.no_encoder:
         enc, eparams, esp = encoder_setup(synth)
         details["encoder"] = encoder_rtfx(torch, synth, enc, dev)
         enc.free()
         if not args.no_details:
             details["clip_batch_24_layers"] = clip_batch_tops(torch, vx, synth, dev, eparams)
+            details["clip_batch_24_layers_g128"] = clip_batch_tops(torch, vx, synth, dev, eparams, group=128)
+            details["attention_core"] = attention_us(torch, dev)
         if not args.no_cpu:
             ce = cpu_encoder_rtfx(eparams, esp, synth)
             details["encoder_cpu"] = ce

@@ -174,8 +174,8 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict
         *(float4 *)&xs[r][q * 4] = px;
         __syncthreads();
         if (k0 + LK < c4) fetch(k0 + LK);
-        const int kend = min(LK, c4 - k0);
-        for (int kk = 0; kk < kend; kk += 4) {
+        // one 4-column step: this lane's weight quad, the four token quads (LDS broadcasts), 16 chained FMAs
+        auto step4 = [&](int kk) __attribute__((always_inline)) {
             const float4 wa = *(const float4 *)&ws[lane][kk];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -185,6 +185,13 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict
                 acc[i][2] = __builtin_fmaf(wa.z, xa.z, acc[i][2]);
                 acc[i][3] = __builtin_fmaf(wa.w, xa.w, acc[i][3]);
             }
+        };
+        if (c4 - k0 >= LK) {
+            // a whole slab: unrolled, so the LDS reads of later steps issue while earlier steps' FMAs run
+#pragma unroll
+            for (int kk = 0; kk < LK; kk += 4) step4(kk);
+        } else {
+            for (int kk = 0; kk < c4 - k0; kk += 4) step4(kk);
         }
         __syncthreads();
     }
