@@ -32,22 +32,23 @@
 namespace vx {
 namespace {
 
-constexpr int kMaxG = 32;  // groups staged in LDS (K <= 4096 with 128-column groups)
+constexpr int kMaxG = 32;  // groups staged in LDS (K <= 4096 with 128-column groups); kernels for K <= 1024 stage 8
 
 // MT x NT blocks of 16 x 16; GROUPED: 128-column groups (else one group); D: K steps per wavefront in flight.
-template <int MT, int NT, bool GROUPED, int D, int EP, bool BIAS, bool QOUT>
+// MAXG: groups the LDS scale tables hold (8 or 32; sized so that a small K leaves room for more workgroups per CU).
+template <int MT, int NT, bool GROUPED, int D, int EP, bool BIAS, bool QOUT, int MAXG>
 __global__ __launch_bounds__(256, 1) void tgemm_small_kernel(const GemmArgs a, const int n_mt, const int per_xcd,
                                                              const int ntiles) {
     constexpr int BM = 16 * MT, BN = 16 * NT, BNP = BN + 4;  // BNP: LDS row pitch (16-byte shift per token row)
     constexpr int TPR = BN / 8;                               // fold threads per token row
     constexpr int RPP = 256 / TPR;                            // token rows per fold pass
     constexpr int R = (BM + RPP - 1) / RPP;                   // fold passes (the last one partial if BM % RPP)
-    constexpr int QX = GROUPED ? kMaxG * BM / 256 : 1, QW = GROUPED ? kMaxG * BN / 256 : 1;
+    constexpr int QX = GROUPED ? (MAXG * BM + 255) / 256 : 1, QW = GROUPED ? (MAXG * BN + 255) / 256 : 1;
     static_assert(!QOUT || (BN == 128 && BM % RPP == 0 && EP != VX_EP_ADD_SCALED),
                   "a quantized output group is one token row of a 128-row tile");
     __shared__ __attribute__((aligned(16))) int red[4][BM * BNP];
-    __shared__ __attribute__((aligned(16))) float sxs[GROUPED ? kMaxG * BM : 1], sws[GROUPED ? kMaxG * BN : 1];
-    __shared__ __attribute__((aligned(16))) int sgs[GROUPED ? kMaxG * BM : 1];
+    __shared__ __attribute__((aligned(16))) float sxs[GROUPED ? MAXG * BM : 1], sws[GROUPED ? MAXG * BN : 1];
+    __shared__ __attribute__((aligned(16))) int sgs[GROUPED ? MAXG * BM : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, lq = lane >> 4;
@@ -176,13 +177,13 @@ __global__ __launch_bounds__(256, 1) void tgemm_small_kernel(const GemmArgs a, c
                 if (i == 1) {
 #pragma unroll
                     for (int q = 0; q < QX; q++)
-                        if (tid + 256 * q < kMaxG * BM) {
+                        if (tid + 256 * q < MAXG * BM) {
                             sxs[tid + 256 * q] = __uint_as_float(qx[q]);
                             sgs[tid + 256 * q] = (int)qg[q];
                         }
 #pragma unroll
                     for (int q = 0; q < QW; q++)
-                        if (tid + 256 * q < kMaxG * BN) sws[tid + 256 * q] = __uint_as_float(qw[q]);
+                        if (tid + 256 * q < MAXG * BN) sws[tid + 256 * q] = __uint_as_float(qw[q]);
                 }
                 to_lds();
                 __syncthreads();
@@ -357,13 +358,14 @@ SmallPlan plan_small(const GemmArgs &a, bool grouped, int force_mt, int force_nt
     return best;
 }
 
-template <int MT, int NT, bool GROUPED, int D>
-void launch_small_ep(const GemmArgs &a, int grid, int n_mt, int per_xcd, int ntiles, hipStream_t st) {
+template <int MT, int NT, bool GROUPED, int D, int MAXG>
+void launch_small_g(const GemmArgs &a, int grid, int n_mt, int per_xcd, int ntiles, hipStream_t st) {
     const bool bias = a.bias != nullptr;
     if constexpr (MT == 1 && NT == 8) {
         if (a.qo) {
 #define VX_SMALLQ(EP)                                                                                             \
-    (bias ? tgemm_small_kernel<MT, NT, GROUPED, D, EP, true, true> : tgemm_small_kernel<MT, NT, GROUPED, D, EP, false, true>)
+    (bias ? tgemm_small_kernel<MT, NT, GROUPED, D, EP, true, true, MAXG>                                          \
+          : tgemm_small_kernel<MT, NT, GROUPED, D, EP, false, true, MAXG>)
             auto k = a.ep == VX_EP_SILU ? VX_SMALLQ(VX_EP_SILU) : VX_SMALLQ(VX_EP_STORE);
 #undef VX_SMALLQ
             k<<<grid, 256, 0, st>>>(a, n_mt, per_xcd, ntiles);
@@ -371,11 +373,21 @@ void launch_small_ep(const GemmArgs &a, int grid, int n_mt, int per_xcd, int nti
         }
     }
 #define VX_SMALL(EP)                                                                                              \
-    (bias ? tgemm_small_kernel<MT, NT, GROUPED, D, EP, true, false> : tgemm_small_kernel<MT, NT, GROUPED, D, EP, false, false>)
+    (bias ? tgemm_small_kernel<MT, NT, GROUPED, D, EP, true, false, MAXG>                                         \
+          : tgemm_small_kernel<MT, NT, GROUPED, D, EP, false, false, MAXG>)
     auto k = a.ep == VX_EP_SILU ? VX_SMALL(VX_EP_SILU) : a.ep == VX_EP_ADD_SCALED ? VX_SMALL(VX_EP_ADD_SCALED)
                                                                                   : VX_SMALL(VX_EP_STORE);
 #undef VX_SMALL
     k<<<grid, 256, 0, st>>>(a, n_mt, per_xcd, ntiles);
+}
+
+// the scale tables for 8 groups when K <= 1024 (the LDS then admits more workgroups per CU), else for 32
+template <int MT, int NT, bool GROUPED, int D>
+void launch_small_ep(const GemmArgs &a, int grid, int n_mt, int per_xcd, int ntiles, hipStream_t st) {
+    if constexpr (GROUPED && D <= 4) {
+        if (a.ng <= 8) return launch_small_g<MT, NT, GROUPED, D, 8>(a, grid, n_mt, per_xcd, ntiles, st);
+    }
+    launch_small_g<MT, NT, GROUPED, D, GROUPED ? kMaxG : 1>(a, grid, n_mt, per_xcd, ntiles, st);
 }
 
 template <int MT, int NT, bool GROUPED>
