@@ -170,6 +170,12 @@ vx_status vx_subsampling(const float *feats, int64_t t, int64_t nm, int64_t c, i
 /* HOST: the relative position table [2t-1, d] (positions t-1 .. -(t-1), sin/cos interleaved per frequency). */
 vx_status vx_rel_pos_table(int64_t t, int64_t d, float *out);
 
+/* DEVICE SELF-CHECK (no counterpart in voxrt): evaluates the library's exp_poly, silu_fast and sigmoid_fast
+ * (tensor.rs:829-860) on the device for all 2^32 float inputs and compares each bit for bit with the IEEE form of
+ * the same formula (NaN equals NaN). mismatch[0..2] receive the mismatch counts of exp, SiLU and sigmoid; all
+ * three are 0 on a correct build. Synchronous, about 0.1 s. */
+vx_status vx_check_activations(uint64_t *mismatch);
+
 /* Device workspace bytes of vx_attention_core for t frames, model width d and h heads. */
 int64_t vx_attention_ws_bytes(int64_t t, int64_t d, int64_t h);
 /* The int8 attention core of one layer for all heads (head dim 128, 1 <= t <= 1024): qkv [t, 3d] (q | k | v),

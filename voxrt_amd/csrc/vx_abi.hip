@@ -37,6 +37,7 @@ int64_t subsampling_scratch_floats(int64_t t, int64_t nm, int64_t c, int64_t k, 
 void fold_bn(const float *dw, const float *gamma, const float *beta, const float *mean, const float *var, int64_t d,
              int64_t k, float *dw_t, float *dw_bias);
 void rel_pos_table(int64_t t, int64_t d, float *out);
+void check_activations(uint64_t *mismatch_host);
 size_t attn_ws_bytes(int64_t t, int64_t d, int64_t h);
 void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h, const float *bias_u,
                     const float *bias_v, float scaling, void *ws, float *ctx, hipStream_t st);
@@ -264,6 +265,13 @@ vx_status vx_rel_pos_table(int64_t t, int64_t d, float *out) {
     return guarded([&] {
         vx::require(out != nullptr && t >= 1 && d > 0 && d % 2 == 0, "vx_rel_pos_table: bad arguments");
         vx::rel_pos_table(t, d, out);
+    });
+}
+
+vx_status vx_check_activations(uint64_t *mismatch) {
+    return guarded([&] {
+        vx::require(mismatch != nullptr, "vx_check_activations: mismatch must not be NULL");
+        vx::check_activations(mismatch);
     });
 }
 

@@ -414,4 +414,36 @@ void rel_pos_table(int64_t t, int64_t d, float *out) {
     }
 }
 
+// Device self-check of the activation functions: exp_poly, silu_fast and sigmoid_fast against their IEEE forms
+// (exp_poly_ieee; x / (1 + exp_poly_ieee(-x)) and 1 / (...) with the IEEE division) over all 2^32 float inputs.
+// NaN results count as equal to NaN; every other result must match bit for bit (the sign of zero included).
+__global__ __launch_bounds__(256) void check_activations_kernel(unsigned long long *mismatch) {
+    const uint64_t nthr = (uint64_t)gridDim.x * 256;
+    unsigned long long c[3] = {0, 0, 0};
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < (1ull << 32); i += nthr) {
+        const float x = __uint_as_float((uint32_t)i);
+        const float got[3] = {exp_poly(x), silu_fast(x), sigmoid_fast(x)};
+        const float want[3] = {exp_poly_ieee(x), silu_ieee(x), sigmoid_ieee(x)};
+#pragma unroll
+        for (int f = 0; f < 3; f++)
+            c[f] += !((got[f] != got[f] && want[f] != want[f]) || __float_as_uint(got[f]) == __float_as_uint(want[f]));
+    }
+#pragma unroll
+    for (int f = 0; f < 3; f++)
+        if (c[f]) atomicAdd(&mismatch[f], c[f]);
+}
+
+void check_activations(uint64_t *mismatch_host) {
+    unsigned long long *dev = nullptr;
+    hip_check(hipMalloc(&dev, 3 * sizeof(unsigned long long)), "hipMalloc");
+    hipError_t e = hipMemset(dev, 0, 3 * sizeof(unsigned long long));
+    if (e == hipSuccess) {
+        check_activations_kernel<<<16384, 256>>>(dev);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpy(mismatch_host, dev, 3 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+    (void)hipFree(dev);
+    hip_check(e, "check_activations");
+}
+
 }  // namespace vx

@@ -61,8 +61,28 @@ __device__ inline float bits_f32(uint32_t u) { return __uint_as_float(u); }
 
 // exp_poly (crates/voxrt/src/tensor.rs:829-848): clamp to [-87, 88], n = rint(x * log2 e), two fma reduction
 // steps, degree-6 Horner by fma, times 2^n. Each step is one IEEE operation (the library is built with
-// -ffp-contract=off), so the result equals the reference bit for bit.
+// -ffp-contract=off), so the result equals the reference bit for bit. exp_poly_ieee is that sequence as written;
+// exp_poly computes the same function in fewer instructions: the NaN-propagating v_maximum3/v_minimum3 clamp
+// (two instructions where two compare-and-select pairs were), and v_ldexp_f32 in place of building 2^n and
+// multiplying. Both forms are exact, so they agree on every input; vx_check_activations compares them over all
+// 2^32 inputs.
+__device__ inline float exp_poly_tail(float x) {
+    float n = __builtin_rintf(x * 1.44269504088896340736f);
+    float r = __builtin_fmaf(-n, 0.69314575f, x);
+    r = __builtin_fmaf(-n, 1.4286068e-6f, r);
+    float p = 1.0f / 720.0f;
+    p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_amdgcn_ldexpf(p, (int)n);
+}
 __device__ inline float exp_poly(float x) {
+    return exp_poly_tail(__builtin_elementwise_minimum(__builtin_elementwise_maximum(x, -87.0f), 88.0f));
+}
+__device__ inline float exp_poly_ieee(float x) {
     x = x < -87.0f ? -87.0f : x;
     x = x > 88.0f ? 88.0f : x;
     float n = __builtin_rintf(x * 1.44269504088896340736f);
@@ -78,9 +98,29 @@ __device__ inline float exp_poly(float x) {
     return p * bits_f32((uint32_t)(((int32_t)n + 127) << 23));
 }
 
-// silu_fast / sigmoid_fast (tensor.rs:852-860), IEEE division.
-__device__ inline float silu_fast(float x) { return x / (1.0f + exp_poly(-x)); }
-__device__ inline float sigmoid_fast(float x) { return 1.0f / (1.0f + exp_poly(-x)); }
+// silu_fast / sigmoid_fast (tensor.rs:852-860): x / (1 + exp_poly(-x)) and 1 / (1 + exp_poly(-x)), correctly
+// rounded as the reference's IEEE division, without a branch (a branch would split the GEMM epilogues' scheduled
+// regions). The divisor d = 1 + exp_poly(-x) lies in [1, 1.7e38]. y = v_rcp_f32(d / 4) / 4 estimates 1/d (the
+// estimate of 4/d is normal over that whole range; 1/d alone would flush to zero for d >= 2^126). SiLU: q = x*y,
+// then one correction by the exact residual fma(-d, q, x) (Markstein's step). The residual is clamped below at
+// -FLT_MAX, which changes nothing for finite x and turns the inf - inf of x = +-inf into a finite correction of
+// q = +-inf; copysign(., x) restores the -0 of x = -0 (SiLU has the sign of x). Sigmoid: one Newton step
+// y + y * fma(-d, y, 1). vx_check_activations compares both with the IEEE forms over all 2^32 inputs.
+__device__ inline float silu_ieee(float x) { return x / (1.0f + exp_poly_ieee(-x)); }
+__device__ inline float sigmoid_ieee(float x) { return 1.0f / (1.0f + exp_poly_ieee(-x)); }
+__device__ inline float recip_est(float d) { return __builtin_amdgcn_rcpf(d * 0.25f) * 0.25f; }
+__device__ inline float silu_fast(float x) {
+    const float d = 1.0f + exp_poly(-x);
+    const float y = recip_est(d);
+    const float q0 = x * y;
+    const float r = __builtin_fmaxf(__builtin_fmaf(-d, q0, x), -3.40282347e38f);
+    return __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
+}
+__device__ inline float sigmoid_fast(float x) {
+    const float d = 1.0f + exp_poly(-x);
+    const float y0 = recip_est(d);
+    return __builtin_fmaf(__builtin_fmaf(-d, y0, 1.0f), y0, y0);
+}
 
 // One quantized code (quantize_group_portable, packed.rs:527-535): clamp(rint(x * inv), -127, 127) with
 // round-half-to-even; NaN -> 0 as Rust's `as i8`.

@@ -74,6 +74,7 @@ def lib() -> C.CDLL:
                                    C.POINTER(I64), P]),
             "vx_rel_pos_table": (I, [I64, I64, P]),
             "vx_attention_ws_bytes": (I64, [I64, I64, I64]),
+            "vx_check_activations": (I, [P]),
             "vx_attention_core": (I, [P, P, I64, I64, I64, P, P, F, P, P, P]),
             "vx_attention_core_quantize": (I, [P, P, I64, I64, I64, P, P, F, P, I64, P, P, P, P]),
             "vx_encoder_create": (I, [P, C.POINTER(P)]),
@@ -347,3 +348,11 @@ def gemm_single(w: TernaryMatrix, x: QuantAct, y, bias=None, stream=None) -> Non
     check(lib().vx_gemm_single(w._h, _dev_ptr(x.x, torch.int8, "x"), _dev_ptr(x.scales_t, torch.float32, "scales_t"),
                                _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), x.n, _dev_ptr(y, torch.float32, "y"),
                                _dev_ptr(bias, torch.float32, "bias"), _stream(stream)))
+
+
+def check_activations() -> tuple:
+    """Device self-check: mismatch counts (exp, SiLU, sigmoid) of the library's activation functions against the
+    IEEE forms of tensor.rs:829-860 over all 2^32 float inputs; (0, 0, 0) on a correct build."""
+    out = (C.c_uint64 * 3)()
+    check(lib().vx_check_activations(C.cast(out, C.c_void_p)))
+    return tuple(int(v) for v in out)
