@@ -284,14 +284,17 @@ def clip_batch_tops(torch, vx, synth, dev, params, reps=3, group=None):
             "pct_int8_peak": round(100 * ops / sec / 1e12 / PEAK_INT8_TOPS, 1)}
 
 
-def cpu_vnni_single_core(synth):
+def cpu_single_core(synth, kernel="vnni"):
     """The reference's per-core CPU GEMM protocol (tests/x86_bench.rs:31-72): FF shapes 4096x1024 and 1024x4096,
     n = 376 tokens, trits lcg % 3 - 1 and x = (lcg % 2001)/100 - 10 from seed 1, f16 scales 0.02, group 128, a
-    256-row slice through the VNNI range kernel on one thread, best of 5; GMAC/s per core, as bench/README.md:122-123
-    quotes (337-359 on a Zen 5 core)."""
+    256-row slice through one x86 range kernel on one thread, best of 5; GMAC/s per core, as bench/README.md:122-123
+    quotes (AVX-512 VNNI 337-359, AVX2 178-181 on a Zen 5 core). kernel: "vnni" (x86.rs:46-154) or "avx2"
+    (x86.rs:163-290), both restated in oracle/."""
     from oracle import oracle
 
-    if not oracle.lib().or_have_vnni():
+    if kernel == "vnni" and not oracle.lib().or_have_vnni():
+        return None
+    if kernel == "avx2" and not oracle.lib().or_have_avx2():
         return None
     rng = synth.Lcg(1)
     out_rates = {}
@@ -306,7 +309,10 @@ def cpu_vnni_single_core(synth):
         best = float("inf")
         for _ in range(5):
             t0 = time.perf_counter()
-            oracle.gemm_vnni_range(wq, sq, out, inp, 128, q, xs, gsum, y, 0, rows, 0, n)
+            if kernel == "vnni":
+                oracle.gemm_vnni_range(wq, sq, out, inp, 128, q, xs, gsum, y, 0, rows, 0, n)
+            else:
+                oracle.gemm_avx2_range(wq, sq, out, inp, 128, True, q, xs, gsum, y, 0, rows, 0, n)
             best = min(best, time.perf_counter() - t0)
         out_rates[f"{out}x{inp}"] = round(rows * inp * n / best / 1e9, 1)
     model = ""
@@ -318,8 +324,9 @@ def cpu_vnni_single_core(synth):
                     break
     except OSError:
         pass
+    name = {"vnni": "AVX-512 VNNI", "avx2": "AVX2"}[kernel]
     return {"gmac_per_s_per_core": out_rates, "threads": 1, "cpu": model, "logical_cpus": os.cpu_count(),
-            "protocol": "x86_bench.rs: n=376, 256-row slice, best of 5, AVX-512 VNNI restatement"}
+            "protocol": f"x86_bench.rs: n=376, 256-row slice, best of 5, {name} restatement"}
 
 
 def attention_us(torch, dev, reps=10):
@@ -495,7 +502,8 @@ def main():
         del extra
     cpu = None if args.no_cpu else cpu_baseline(gemms)
     if not args.no_cpu and not args.no_details:
-        details["cpu_vnni_single_core"] = cpu_vnni_single_core(synth)
+        details["cpu_vnni_single_core"] = cpu_single_core(synth, "vnni")
+        details["cpu_avx2_single_core"] = cpu_single_core(synth, "avx2")
     if not args.no_encoder:
         enc, eparams, esp = encoder_setup(synth)
         details["encoder"] = encoder_rtfx(torch, synth, enc, dev)

@@ -52,6 +52,8 @@ def lib() -> C.CDLL:
             "or_quad16_pack": (None, [P, S, S, S, P, P, P]),
             "or_gemm_vnni_range": (None, [P, P, S, S, S, P, P, P, S, P, S, S, S, S, I, F]),
             "or_gemm_ep_vnni": (None, [P, P, S, S, S, P, P, P, S, P, I, F, I, S]),
+            "or_have_avx2": (I, []),
+            "or_gemm_avx2_range": (I, [P, P, S, S, S, I, P, P, P, S, P, S, S, S, S, I, F]),
             "or_get_threads": (I, []),
             "or_set_threads": (None, [I]),
             "or_row_mean_var": (None, [P, S, P, P]),
@@ -163,6 +165,13 @@ def gemm_vnni_range(wq, sq, out, inp, group, x, xs, gsum, y, r0, r1, t0, t1, ep=
     n = x.shape[0]
     lib().or_gemm_vnni_range(_p(wq), _p(sq), out, inp, group, _p(x), _p(xs), _p(gsum), n, _p(y), r0, r1, t0, t1,
                              ep, alpha)
+
+
+def gemm_avx2_range(wq, sq, out, inp, group, ternary, x, xs, gsum, y, r0, r1, t0, t1, ep=EP_STORE, alpha=0.0):
+    """The AVX2 restatement (x86.rs:163-290); returns -1 (nothing written) for ternary weights with group > 256."""
+    n = x.shape[0]
+    return lib().or_gemm_avx2_range(_p(wq), _p(sq), out, inp, group, int(bool(ternary)), _p(x), _p(xs), _p(gsum), n,
+                                    _p(y), r0, r1, t0, t1, ep, alpha)
 
 
 def gemm_ep_vnni(wq, sq, out, inp, group, x, xs, gsum, y, ep=EP_STORE, alpha=0.0, threads=1, blocks_mult=8):

@@ -18,6 +18,7 @@
  *   or_exp_poly : relative error < 3e-7 against exp in double (tensor.rs:1018-1030).
  *   or_lcg : the numpy jump-ahead generator (voxrt_amd/synth.py) must reproduce its stream exactly.
  *   or_gemm_vnni_range (CPU baseline) : bit-identical to or_gemm_scalar_range on the x86_kernels.rs grid.
+ *   or_gemm_avx2_range (CPU, AVX2)     : bit-identical to or_gemm_scalar_range on the same grid.
  *
  * Encoder side (encoder_oracle.c):
  *   or_row_mean_var / or_layer_norm : float64 LayerNorm within 1e-5; constant rows give exactly b; a numpy float32
@@ -77,6 +78,13 @@ void or_gemm_vnni_range(const int8_t *wq, const float *scales_q, size_t out, siz
 void or_gemm_ep_vnni(const int8_t *wq, const float *scales_q, size_t out, size_t inp, size_t group,
                      const int8_t *x, const float *xs, const int32_t *gsum, size_t n, float *y, int ep, float alpha,
                      int threads, size_t blocks_mult);
+
+/* Second CPU path: AVX2 restatement on the same Quad16 plane (kernels/x86.rs:163-290); -1 for ternary with
+ * group > 256, else 0 */
+int or_have_avx2(void);
+int or_gemm_avx2_range(const int8_t *wq, const float *scales_q, size_t out, size_t inp, size_t group, int ternary,
+                       const int8_t *x, const float *xs, const int32_t *gsum, size_t n, float *y, size_t r0, size_t r1,
+                       size_t t0, size_t t1, int ep, float alpha);
 
 /* Thread count of the oracle's parallel loops (default 1; results do not depend on it). */
 int or_get_threads(void);

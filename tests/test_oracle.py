@@ -293,7 +293,7 @@ def _acts(rng, n, inp, extreme=False):
     return synth.ref_acts(rng, n, inp)
 
 
-def _check_vnni(orc, rng, rows, ws, group, xf):
+def _check_vnni(orc, rng, rows, ws, group, xf, kernel=None):
     out, inp = rows.shape
     n = xf.shape[0]
     q, xs, gsum = orc.quantize(xf, group)
@@ -308,7 +308,10 @@ def _check_vnni(orc, rng, rows, ws, group, xf):
             want = init.copy()
             orc.gemm_scalar_range(rows, ws, q, xs, group, want, r0, r1, t0, t1, ep, alpha)
             got = init.copy()
-            orc.gemm_vnni_range(wq, sq, out, inp, group, q, xs, gsum, got, r0, r1, t0, t1, ep, alpha)
+            if kernel is None:
+                orc.gemm_vnni_range(wq, sq, out, inp, group, q, xs, gsum, got, r0, r1, t0, t1, ep, alpha)
+            else:
+                assert kernel(wq, sq, out, inp, group, q, xs, gsum, got, r0, r1, t0, t1, ep, alpha) == 0
             assert got.view(np.uint32).tolist() == want.view(np.uint32).tolist(), (out, inp, group, n, r0, r1, t0, t1, ep)
 
 
@@ -361,3 +364,62 @@ def test_vnni_threaded_gemm_ep_equals_scalar(orc):
     got = np.zeros((n, out), np.float32)
     orc.gemm_ep_vnni(wq, sq, out, inp, 128, q, xs, gsum, got, threads=4)
     assert got.view(np.uint32).tolist() == want.view(np.uint32).tolist()
+
+
+# the AVX2 path (x86.rs:163-290) on the same grids (x86_kernels.rs runs both kernels through one check)
+
+def _need_avx2(orc):
+    if not orc.lib().or_have_avx2():
+        pytest.skip("no AVX2/FMA on this host")
+
+
+def _avx2(orc, ternary):
+    return lambda *a: orc.gemm_avx2_range(*a[:5], ternary, *a[5:])
+
+
+def test_avx2_ternary_equals_scalar_exactly(orc):
+    """x86_kernels.rs:140-152 for gemm_avx2_range (ternary weights, int16 sums per group)."""
+    _need_avx2(orc)
+    rng = synth.Lcg(3)
+    for out, inp in [(7, 128), (16, 256), (33, 1024), (130, 4096)]:
+        trits, ws = _ternary_q16(orc, rng, out, inp)
+        for n in [1, 2, 3, 4, 5, 8, 9, 17]:
+            _check_vnni(orc, rng, trits, ws, 128, _acts(rng, n, inp), _avx2(orc, True))
+
+
+def test_avx2_int8_equals_scalar_exactly(orc):
+    """x86_kernels.rs:154-172 for gemm_avx2_range (int8 weights, groups 128, 384, 1024)."""
+    _need_avx2(orc)
+    rng = synth.Lcg(5)
+    for out, inp, group in [(7, 128, 128), (40, 640, 128), (128, 384, 384), (19, 1024, 1024)]:
+        rows, ws = _int8_q16(rng, out, inp, group)
+        for n in [1, 2, 5, 8, 11]:
+            _check_vnni(orc, rng, rows, ws, group, _acts(rng, n, inp), _avx2(orc, False))
+
+
+def test_avx2_extremes_do_not_saturate(orc):
+    """x86_kernels.rs:174-185 for gemm_avx2_range: all-ones trits and +-127 weights against +-127 codes, where
+    vpmaddubsw would saturate if the pairs were not bounded."""
+    _need_avx2(orc)
+    rng = synth.Lcg(9)
+    trits, ws = _ternary_q16(orc, rng, 32, 1024, extreme=True)
+    _check_vnni(orc, rng, trits, ws, 128, _acts(rng, 5, 1024, extreme=True), _avx2(orc, True))
+    trits, ws = _ternary_q16(orc, rng, 16, 512, extreme=True)
+    ws = np.repeat(ws[:, :1], 2, axis=1)
+    _check_vnni(orc, rng, trits, ws, 256, _acts(rng, 3, 512, extreme=True), _avx2(orc, True))
+    rows, ws = _int8_q16(rng, 32, 1024, 1024, extreme=True)
+    _check_vnni(orc, rng, rows, ws, 1024, _acts(rng, 5, 1024, extreme=True), _avx2(orc, False))
+
+
+def test_avx2_ternary_needs_group_at_most_256(orc):
+    """Ternary int16 group sums bound the AVX2 path to group <= 256 (x86.rs:173-174, kernels/mod.rs:326-328): a
+    larger group is refused and y is left untouched."""
+    _need_avx2(orc)
+    rng = synth.Lcg(11)
+    trits, ws = _ternary_q16(orc, rng, 16, 1024)
+    ws1 = ws[:, :1].copy()
+    q, xs, gsum = orc.quantize(_acts(rng, 2, 1024), 1024)
+    wq, sq = orc.quad16_pack(trits, ws1, 1024)
+    y = np.full((2, 16), 7.0, np.float32)
+    assert orc.gemm_avx2_range(wq, sq, 16, 1024, 1024, True, q, xs, gsum, y, 0, 16, 0, 2) == -1
+    assert (y == 7.0).all()
