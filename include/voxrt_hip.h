@@ -4,6 +4,7 @@
  * crates/voxrt/src/packed.rs), so a GPU backend binds beside its scalar/AVX2/VNNI/NEON kernels:
  *
  *   vx_detect / vx_init               <- kernels::detect (kernels/mod.rs:85-109)
+ *   vx_shutdown                       <- (none: drains the device at the end of a session)
  *   vx_tmat_upload_packed             <- TernaryMatrix::from_packed_layout (packed.rs:73-130)
  *   vx_tmat_upload_packed_f32         <- the same with f32 scales (BASELINE config 0's per-channel fp32 scale)
  *   vx_tmat_upload_i8                 <- TernaryMatrix::from_i8_rows (packed.rs:164-201)
@@ -24,6 +25,7 @@
  *   vx_encoder_*                      <- GpuEncoder::{load, forward, forward_feats} (metal/mod.rs:446-603) on the
  *                                        CPU int8 Encoder's operation order (encoder.rs:706-857)
  *   vx_last_error                     <- voxrt_last_error (crates/voxrt-ffi/src/lib.rs:61-74)
+ *   vx_check_activations              <- (none: device self-check of exp_poly/silu_fast/sigmoid_fast)
  *
  * Conventions (as voxrt-ffi): every call returns a vx_status; on failure a message is kept in a thread-local
  * buffer read by vx_last_error(). No exception crosses the ABI. Weight uploads take HOST pointers (the load-time
@@ -66,6 +68,11 @@ int vx_detect(void);
 
 /* Make `device` current for this thread and check that it is gfx950. */
 vx_status vx_init(int device);
+
+/* Wait for all work on the current device and report any error it left. No counterpart in voxrt (its GPU
+ * context lives until the process drops it); for hosts that end a device session explicitly. The library keeps no
+ * global device memory: weight and encoder handles are released by their _free calls. */
+vx_status vx_shutdown(void);
 
 /* from_packed_layout: qweight = thrush-ternary-v2 rows uint8 [out, ceil(inp/5)] (5 trits per byte, least
  * significant base-3 digit first, trit = digit - 1), scales_f16 = IEEE binary16 [out, inp/group]. */

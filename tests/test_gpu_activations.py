@@ -16,3 +16,10 @@ def test_activations_equal_ieee_forms_on_all_inputs():
     assert vx.detect() == vx.Kernel.Hip, "no gfx950 device"
     vx.kernels.check(vx.lib().vx_init(0))
     assert vx.kernels.check_activations() == (0, 0, 0)
+
+
+def test_shutdown_drains_the_device():
+    import voxrt_amd as vx
+
+    vx.kernels.check(vx.lib().vx_init(0))
+    vx.kernels.check(vx.lib().vx_shutdown())

@@ -117,6 +117,10 @@ vx_status vx_init(int device) {
     });
 }
 
+vx_status vx_shutdown(void) {
+    return guarded([&] { vx::hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize"); });
+}
+
 vx_status vx_tmat_upload_packed(const uint8_t *qweight, const uint16_t *scales_f16, int64_t out, int64_t inp,
                                 int64_t group, vx_tmat **w) {
     return guarded([&] {

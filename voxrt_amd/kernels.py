@@ -52,6 +52,7 @@ def lib() -> C.CDLL:
             "vx_last_error": (C.c_char_p, []),
             "vx_detect": (I, []),
             "vx_init": (I, [I]),
+            "vx_shutdown": (I, []),
             "vx_tmat_upload_packed": (I, [P, P, I64, I64, I64, C.POINTER(P)]),
             "vx_tmat_upload_packed_f32": (I, [P, P, I64, I64, I64, C.POINTER(P)]),
             "vx_tmat_upload_i8": (I, [P, P, I64, I64, I64, C.POINTER(P)]),
