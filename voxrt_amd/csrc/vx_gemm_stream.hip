@@ -47,6 +47,8 @@ namespace {
 // later step (3 DMA + 2 stores), plus the 4 scale DMAs issued after the loads of tile step nk-kPD.
 constexpr int kPD = 6;
 constexpr int kEarly = 2;  // token rows of MFMAs issued before a step's loads (the matrix pipe stays busy)
+constexpr int kValuPerDs = 2;    // VALU instructions placed beside each fragment read (with its MFMA)
+constexpr int kValuPerMfma = 3;  // VALU instructions after each remaining MFMA (one MFMA is 16 cycles)
 __device__ constexpr int wait_of(int i, int nk) { return 2 + 5 * (kPD - 2) + ((i >= nk - kPD + 1) ? 4 : 0); }
 
 template <int EP, bool BIAS, bool K16>
@@ -261,17 +263,18 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
             __builtin_amdgcn_raw_buffer_store_b128(z, yrs, kOff, 0, 0);
         }
         widen(fs ^ 1);
-        // issue order: the 8 fragment reads of the next step each after an MFMA, then 3 VALU after each of the
-        // remaining MFMAs (epilogue and widening work hides under the matrix pipe)
+        // issue order: the 8 fragment reads of the next step each after an MFMA with 2 VALU, then 3 VALU after
+        // each of the remaining MFMAs (epilogue and widening work hides under the matrix pipe)
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, kValuPerDs, 0);
         }
 #pragma unroll
         for (int k = 0; k < 24 - 4 * kEarly; k++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
