@@ -34,7 +34,9 @@
  * ordered on that stream and returns before the work completes. Calls on different streams that write disjoint
  * outputs may run concurrently; a vx_tmat is immutable after upload and may be shared by any number of calls.
  *
- * Shape rules: inp % group == 0, group % 64 == 0 (one i8 MFMA step is 64 columns).
+ * Shape rules: inp % group == 0, group % 64 == 0 (one i8 MFMA step is 64 columns). A call over zero tokens
+ * (n = 0, t = 0, or an empty row or token range) does nothing and returns VX_OK; its activation, output and
+ * parameter pointers may then be NULL (the reference's kernels loop over zero tokens).
  */
 #ifndef VOXRT_HIP_H
 #define VOXRT_HIP_H

@@ -68,3 +68,16 @@ def test_epilogue_values_match_header():
     hdr = open(os.path.join(ROOT, "include", "voxrt_hip.h")).read()
     assert "VX_EP_STORE = 0" in hdr and "VX_EP_SILU = 1" in hdr and "VX_EP_ADD_SCALED = 2" in hdr
     assert vx.Epilogue.Store.kind == 0 and vx.Epilogue.Silu.kind == 1 and vx.Epilogue.AddScaled(0.5).kind == 2
+
+
+def test_zero_tokens_take_null_pointers():
+    """n = 0 / t = 0 is a no-op that returns VX_OK with NULL data pointers and touches no device (as the
+    reference's kernels loop over zero tokens); with one token the same NULL pointers are refused."""
+    L = vx.lib()
+    assert L.vx_quantize(None, 0, 128, 128, None, None, None, None) == 0
+    assert L.vx_quantize_normed(None, 0, 128, 128, None, None, None, None, None, None) == 0
+    assert L.vx_layer_norm(None, 0, 1024, None, None, None, None) == 0
+    assert L.vx_linear_f32(None, 0, 64, None, None, 32, None, 0, None) == 0
+    assert L.vx_glu_dwconv_silu(None, 0, 256, 9, None, None, None, None) == 0
+    assert L.vx_quantize(None, 1, 128, 128, None, None, None, None) == kernels.VX_ERR_INVALID
+    assert L.vx_layer_norm(None, 1, 1024, None, None, None, None) == kernels.VX_ERR_INVALID

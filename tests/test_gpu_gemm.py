@@ -543,3 +543,32 @@ def test_gemm_ep_quantize_equals_two_step(dev, orc, m, k, n_out, group, ep_kind,
     _assert_bits_equal(st[:, :m].T.copy(), wsc, f"scales {tag}")
     np.testing.assert_array_equal(gt[:, :m].T, wgs, err_msg=f"gsum {tag}")
     assert not st[:, m:].any() and not gt[:, m:].any(), f"pad tokens not zero {tag}"
+
+
+def test_zero_tokens_is_a_no_op(dev):
+    """A batch of zero tokens (the reference's kernels loop over nothing): quantize, gemm_ep with every epilogue,
+    the fused GEMM -> quantize, gemm_single and the empty row / token ranges of gemm_rows_range return without
+    touching y, also with the NULL data pointers of empty torch tensors."""
+    import torch
+
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(77)
+    out, inp = 256, 1024
+    qw, s16, _ = synth.ref_random_matrix(rng, out, inp)
+    w = vx.TernaryMatrix.from_packed(qw, s16, out, inp, 128)
+    x0 = vx.QuantAct.quantize(torch.empty((0, inp), dtype=torch.float32, device=dev), 128)
+    assert x0.n == 0
+    y0 = torch.empty((0, out), dtype=torch.float32, device=dev)
+    for ep in (vx.Epilogue.Store, vx.Epilogue.Silu, vx.Epilogue.AddScaled(0.5)):
+        vx.gemm_ep(w, x0, y0, None, ep)
+    qa = vx.gemm_ep_quantize(w, x0)
+    assert qa.n == 0
+    vx.gemm_single(w, x0, y0)
+    # empty ranges of a non-empty batch leave y as it was
+    x = vx.QuantAct.quantize(torch.from_numpy(synth.ref_acts(rng, 5, inp)).to(dev), 128)
+    y = torch.full((5, out), 3.0, dtype=torch.float32, device=dev)
+    vx.gemm_rows_range(w, x, y, 7, 7, 0, 5)
+    vx.gemm_rows_range(w, x, y, 0, out, 2, 2)
+    torch.cuda.synchronize()
+    assert bool((y == 3.0).all())

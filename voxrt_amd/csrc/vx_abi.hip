@@ -207,7 +207,7 @@ vx_status vx_gemm_single(const vx_tmat *w, const int8_t *xq, const float *xs_t, 
 vx_status vx_quantize_normed(const float *x, int64_t n, int64_t inp, int64_t group, const float *gamma,
                              const float *beta, int8_t *q, float *scales_t, int32_t *gsum_t, void *stream) {
     return guarded([&] {
-        vx::require(gamma && beta, "gamma and beta must not be NULL");
+        vx::require(n == 0 || (gamma && beta), "gamma and beta must not be NULL");
         vx::quantize_ln(x, n, inp, group, gamma, beta, q, scales_t, gsum_t, (hipStream_t)stream);
     });
 }
@@ -215,7 +215,7 @@ vx_status vx_quantize_normed(const float *x, int64_t n, int64_t inp, int64_t gro
 vx_status vx_layer_norm(const float *x, int64_t n, int64_t d, const float *gamma, const float *beta, float *y,
                         void *stream) {
     return guarded([&] {
-        vx::require(x != y, "vx_layer_norm: y must not alias x");
+        vx::require(n == 0 || x != y, "vx_layer_norm: y must not alias x");
         vx::layer_norm(x, n, d, gamma, beta, y, (hipStream_t)stream);
     });
 }

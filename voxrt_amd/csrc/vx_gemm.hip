@@ -1251,8 +1251,8 @@ static GemmArgs gemm_args(const TMat *w, const int8_t *xq, const float *xs_t, co
                           float *y, const float *bias, int ep, float alpha, int32_t *gs, int64_t r0, int64_t r1,
                           int64_t t0, int64_t t1, bool y_needed) {
     require(w != nullptr, "weight matrix must not be NULL");
-    require(xq && xs_t && (y || !y_needed), "xq, xs_t and y must not be NULL");
-    require(!w->ternary || xg_t, "ternary weights need the activation code sums (xgsum_t)");
+    require(n == 0 || (xq && xs_t && (y || !y_needed)), "xq, xs_t and y must not be NULL");
+    require(n == 0 || !w->ternary || xg_t, "ternary weights need the activation code sums (xgsum_t)");
     require(ep == VX_EP_STORE || ep == VX_EP_SILU || ep == VX_EP_ADD_SCALED, "unknown epilogue");
     require(n >= 0, "n must be >= 0");
     require(0 <= r0 && r0 <= r1 && r1 <= w->out, "row range outside [0, out]");
@@ -1367,7 +1367,7 @@ void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const fl
 // shapes run the GEMM into y_tmp and then the quantizer. The codes equal those of the two-step chain bit for bit.
 void gemm_quant(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y_tmp,
                 const float *bias, int ep, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st) {
-    require(q && scales_t && gsum_t, "q, scales_t and gsum_t must not be NULL");
+    require(n == 0 || (q && scales_t && gsum_t), "q, scales_t and gsum_t must not be NULL");
     require(ep == VX_EP_STORE || ep == VX_EP_SILU, "a quantized output takes the Store or Silu epilogue");
     require(w != nullptr && group > 0 && w->out % group == 0, "out must be a positive multiple of group");
     GemmArgs a = gemm_args(w, xq, xs_t, xg_t, n, y_tmp, bias, ep, 0.0f, nullptr, 0, w->out, 0, n, false);

@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void glu_dwconv_silu_kernel(const float *__res
 // nseg segments of t frames each: g [nseg][t][2d] -> out [nseg][t][d].
 void glu_dwconv_silu_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
                          const float *bias, float *out, hipStream_t st) {
-    require(g && w_t && bias && out, "glu_dwconv: NULL pointer");
+    require(t == 0 || (g && w_t && bias && out), "glu_dwconv: NULL pointer");
     require(nseg >= 1 && t >= 0 && d > 0 && k > 0 && k % 2 == 1 && nseg * t * 2 * d < (1ll << 31) &&
                 nseg * t <= 65535,
             "glu_dwconv: bad shape");
@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void glu_dwconv_silu_quant_kernel(const float 
 // [nseg * t][d], scales_t and gsum_t [d / 128][npad(nseg * t)].
 void glu_dwconv_silu_quant_seg(const float *g, int64_t nseg, int64_t t, int64_t d, int64_t k, const float *w_t,
                                const float *bias, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st) {
-    require(g && w_t && bias && q && scales_t && gsum_t, "glu_dwconv_quantize: NULL pointer");
+    require(t == 0 || (g && w_t && bias && q && scales_t && gsum_t), "glu_dwconv_quantize: NULL pointer");
     require(nseg >= 1 && t >= 0 && d > 0 && d % 256 == 0 && k > 0 && k % 2 == 1 && nseg * t * 2 * d < (1ll << 31) &&
                 nseg * t <= 65535,
             "glu_dwconv_quantize: bad shape (d a multiple of 256)");
@@ -246,7 +246,7 @@ __global__ void gemv_f32_kernel(const float *__restrict__ x, int in_f, const flo
 
 void linear_f32(const float *x, int64_t n, int64_t in_f, const float *w, const float *b, int64_t out_f, float *y,
                 bool relu, hipStream_t st) {
-    require(x && w && y, "linear_f32: NULL pointer");
+    require(n == 0 || (x && w && y), "linear_f32: NULL pointer");
     require(n >= 0 && in_f > 0 && out_f > 0 && n * in_f < (1ll << 31) && n * out_f < (1ll << 31) &&
                 out_f * in_f < (1ll << 31),
             "linear_f32: bad shape");

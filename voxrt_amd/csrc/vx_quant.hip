@@ -398,7 +398,7 @@ __global__ void quantize_pad_kernel(int n, int np, int ng, float *__restrict__ s
 // Launches the quantizer; with g and b, the LN variant (both NULL: plain quantization).
 void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const float *g, const float *b, int8_t *q,
                  float *scales_t, int32_t *gsum_t, hipStream_t stream) {
-    require(x && q && scales_t && gsum_t, "x, q, scales_t and gsum_t must not be NULL");
+    require(n == 0 || (x && q && scales_t && gsum_t), "x, q, scales_t and gsum_t must not be NULL");
     require((g == nullptr) == (b == nullptr), "LayerNorm needs both gamma and beta");
     require(n >= 0 && inp > 0 && group > 0 && inp % group == 0, "inp must be a positive multiple of group");
     require(n * inp < (1ll << 31), "activation block above 2 GiB");
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict
 }
 
 void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y, hipStream_t stream) {
-    require(x && g && b && y, "x, gamma, beta and y must not be NULL");
+    require(n == 0 || (x && g && b && y), "x, gamma, beta and y must not be NULL");
     require(n >= 0 && d > 0 && n * d < (1ll << 31), "bad LayerNorm shape");
     if (n == 0) return;
     auto al16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
@@ -510,7 +510,7 @@ void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const floa
 void layer_norm_quantize_ln(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y,
                             int64_t group, const float *g2, const float *b2, int8_t *q, float *scales_t,
                             int32_t *gsum_t, hipStream_t stream) {
-    require(x && g && b && y && g2 && b2 && q && scales_t && gsum_t, "LayerNorm -> quantize: NULL pointer");
+    require(n == 0 || (x && g && b && y && g2 && b2 && q && scales_t && gsum_t), "LayerNorm -> quantize: NULL pointer");
     require(n >= 0 && d > 0 && group > 0 && d % group == 0 && n * d < (1ll << 31), "bad LayerNorm shape");
     if (n == 0) return;
     auto al16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
