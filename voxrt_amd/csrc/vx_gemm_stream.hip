@@ -27,11 +27,11 @@
 //   * within a step: the LDS reads that its VALU work waits for (epilogue scales, next step's weight codes) come
 //     first, two rows of MFMAs run while the step's loads issue, and the next step's fragment reads and the VALU
 //     work are interleaved with the remaining MFMAs;
-//   * two accumulator sets alternate between tiles: while the MFMAs of tile j accumulate into one, the epilogue of
-//     tile j - 1 (subtract gsum, fold fma((float)S, xs * ws, 0), Store or SiLU, bias) is computed from the other, two
-//     output blocks per step over the first 16 steps, and its 16-byte stores leave between the MFMAs. The f32 output
-//     stream thus overlaps the next tile's MFMA work instead of following it. AddScaled (which reads y) is applied
-//     once per tile after its last step.
+//   * Store with K = 1024: two accumulator sets alternate between tiles; while the MFMAs of tile j accumulate into
+//     one, the epilogue of tile j - 1 (subtract gsum, fold fma((float)S, xs * ws, 0), bias) is computed from the
+//     other, two output blocks per step over the first 16 steps, and its 16-byte stores leave between the MFMAs, so
+//     the f32 output stream overlaps the next tile's MFMA work. SiLU, AddScaled (which reads y) and K > 1024 use
+//     one accumulator set and write each tile's epilogue after its last step (measured faster for those).
 // Token scales, gsum, weight scales and bias of a tile are brought to LDS by DMA six steps before the tile ends.
 #include <algorithm>
 #include <cstring>
@@ -53,6 +53,11 @@ __device__ constexpr int wait_of(int i, int nk) { return 2 + 5 * (kPD - 2) + ((i
 
 template <int EP, bool BIAS, bool K16>
 __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, const StreamGeom g) {
+    // DRAIN: every tile's epilogue after its last step, one accumulator set. Measured at 8192 tokens: faster for
+    // SiLU (its VALU work made the steps of the next tile VALU-bound: 67 -> 62 us for FFN-up) and for K > 1024
+    // (FFN-down 32.7 -> 31.4 us); the Store epilogue with K = 1024 keeps the two-blocks-per-step overlap
+    // (40 us against 43).
+    constexpr bool DRAIN = EP != VX_EP_STORE || !K16;
     typedef __attribute__((address_space(3))) void lds_void;
     // one LDS object per activation slot and per scale table: the compiler then sees that a DMA into one slot
     // does not alias the fragment reads of another and adds no vmcnt wait of its own before them
@@ -225,7 +230,7 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         // LDS reads that this step's VALU work waits for: the pending block pair's scales, next step's weights
-        constexpr bool CHUNK = CH >= 0 && EP != VX_EP_ADD_SCALED;
+        constexpr bool CHUNK = CH >= 0 && !DRAIN;
         BlockScales sc0, sc1;
         if constexpr (CHUNK) {
             sc0 = block_scales(PAR ^ 1, CH / 2, 2 * (CH % 2));
@@ -321,7 +326,7 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
             });
         }
         // this tile becomes the pending one (or is written now: AddScaled, or the last tile)
-        if (EP == VX_EP_ADD_SCALED || nxt < 0) {
+        if (DRAIN || nxt < 0) {
             drain(IC<PAR>{}, acc);
             vy_p = kOff;
         } else {
@@ -361,7 +366,10 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
     for (;;) {
         run_tile(IC<0>{}, acc0, acc1);
         if (cur < 0) break;
-        run_tile(IC<1>{}, acc1, acc0);
+        if constexpr (DRAIN)
+            run_tile(IC<1>{}, acc0, acc1);
+        else
+            run_tile(IC<1>{}, acc1, acc0);
         if (cur < 0) break;
     }
     __builtin_amdgcn_s_waitcnt(0);
