@@ -19,6 +19,8 @@
 //                       [t-1-i_max, 2t-2-i0] through v_mfma_i32_16x16x64_i8 into LDS; softmax in LDS (the four
 //                       running sums per row on four lanes, so the order is the reference's); the probabilities
 //                       quantized into LDS; P . vT through the same MFMA; ctx written in place in [t][d].
+#include <atomic>
+
 #include "vx_internal.h"
 
 namespace vx {
@@ -471,15 +473,19 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
                                                                          rows_blocks);
     hip_check(hipGetLastError(), "attention rows / vT kernel launch");
     const size_t lds = core_lds_bytes((int)t);
-    static bool lds_raised = false;
-    if (!lds_raised) {
+    // the dynamic-LDS limit of the core kernels, raised once per device (thread-safe; devices past 63 every call)
+    static std::atomic<bool> lds_raised[64];
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    const bool cached = dev >= 0 && dev < 64;
+    if (!cached || !lds_raised[dev].load(std::memory_order_acquire)) {
         hip_check(hipFuncSetAttribute((const void *)attn_core_kernel<false>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
                   "attention LDS limit");
         hip_check(hipFuncSetAttribute((const void *)attn_core_kernel<true>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
                   "attention LDS limit");
-        lds_raised = true;
+        if (cached) lds_raised[dev].store(true, std::memory_order_release);
     }
     AttnQOut Q{q, scales_t, gsum_t, (int)((nseg * t + 15) / 16 * 16)};
     const dim3 grid((unsigned)(D.tp / 16), (unsigned)h, (unsigned)nseg);

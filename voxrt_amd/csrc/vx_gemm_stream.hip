@@ -34,6 +34,7 @@
 //     one accumulator set and write each tile's epilogue after its last step (measured faster for those).
 // Token scales, gsum, weight scales and bias of a tile are brought to LDS by DMA six steps before the tile ends.
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <utility>
 
@@ -385,14 +386,18 @@ void launch_stream(const GemmArgs &a, const StreamGeom &g, int grid, hipStream_t
 
 }  // namespace
 
+// CU count of the current device, cached per device (a host thread may switch devices between calls)
 int cu_count() {
-    static int n = 0;
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    const bool cached = dev >= 0 && dev < 64;
+    int n = cached ? cache[dev].load(std::memory_order_relaxed) : 0;
     if (n == 0) {
-        int dev = 0;
-        hip_check(hipGetDevice(&dev), "hipGetDevice");
         int c = 0;
         hip_check(hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
         n = c > 0 ? c : 256;
+        if (cached) cache[dev].store(n, std::memory_order_relaxed);
     }
     return n;
 }
