@@ -110,7 +110,9 @@ __device__ inline float silu_ieee(float x) { return x / (1.0f + exp_poly_ieee(-x
 __device__ inline float sigmoid_ieee(float x) { return 1.0f / (1.0f + exp_poly_ieee(-x)); }
 __device__ inline float recip_est(float d) { return __builtin_amdgcn_rcpf(d * 0.25f) * 0.25f; }
 __device__ inline float silu_fast(float x) {
-    const float d = 1.0f + exp_poly(-x);
+    // the clamp by one v_med3_f32: it differs from the NaN-propagating form only for x = NaN, where q0 = x * y
+    // makes the quotient NaN whatever d is
+    const float d = 1.0f + exp_poly_tail(__builtin_amdgcn_fmed3f(-x, -87.0f, 88.0f));
     const float y = recip_est(d);
     const float q0 = x * y;
     const float r = __builtin_fmaxf(__builtin_fmaf(-d, q0, x), -3.40282347e38f);
