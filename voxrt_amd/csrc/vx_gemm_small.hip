@@ -36,9 +36,11 @@ constexpr int kMaxG = 32;  // groups staged in LDS (K <= 4096 with 128-column gr
 
 // MT x NT blocks of 16 x 16; GROUPED: 128-column groups (else one group); D: K steps per wavefront in flight.
 // MAXG: groups the LDS scale tables hold (8 or 32; sized so that a small K leaves room for more workgroups per CU).
+// 16 x 128 tiles with a ring of at most 4 steps (one group, or a quantized output) are held to 168 registers, so
+// that three workgroups fit per CU and a T = 338 grid of 704 tiles runs in one round.
 template <int MT, int NT, bool GROUPED, int D, int EP, bool BIAS, bool QOUT, int MAXG>
-__global__ __launch_bounds__(256, 1) void tgemm_small_kernel(const GemmArgs a, const int n_mt, const int per_xcd,
-                                                             const int ntiles) {
+__global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || QOUT)) ? 3 : 1) void tgemm_small_kernel(
+    const GemmArgs a, const int n_mt, const int per_xcd, const int ntiles) {
     constexpr int BM = 16 * MT, BN = 16 * NT, BNP = BN + 4;  // BNP: LDS row pitch (16-byte shift per token row)
     constexpr int TPR = BN / 8;                               // fold threads per token row
     constexpr int RPP = 256 / TPR;                            // token rows per fold pass
