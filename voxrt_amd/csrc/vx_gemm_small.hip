@@ -48,7 +48,12 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
     constexpr int QX = GROUPED ? (MAXG * BM + 255) / 256 : 1, QW = GROUPED ? (MAXG * BN + 255) / 256 : 1;
     static_assert(!QOUT || (BN == 128 && BM % RPP == 0 && EP != VX_EP_ADD_SCALED),
                   "a quantized output group is one token row of a 128-row tile");
-    __shared__ __attribute__((aligned(16))) int red[4][BM * BNP];
+    // NRED = 2: with 32-group tables (K > 1024, eight or more chunks) the chunks alternate between two reduction
+    // planes, so a chunk's fold needs no barrier after it (the next chunk writes the other plane, and the barrier
+    // after that write orders it after every thread's reads of the plane it overwrites two chunks later); only for
+    // tiles whose two planes and tables fit in LDS next to each other (at most 88 KB)
+    constexpr int NRED = (GROUPED && MAXG > 8 && BM * BNP <= 2176) ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) int red[NRED][4][BM * BNP];
     __shared__ __attribute__((aligned(16))) float sxs[GROUPED ? MAXG * BM : 1], sws[GROUPED ? MAXG * BN : 1];
     __shared__ __attribute__((aligned(16))) int sgs[GROUPED ? MAXG * BM : 1];
 
@@ -153,12 +158,12 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
         for (int j = 0; j < 8; j++) accf[r][j] = 0.0f;
 
     // int32 sums of this wavefront -> its LDS plane (one 16-byte write per block)
-    auto to_lds = [&]() __attribute__((always_inline)) {
+    auto to_lds = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int mb = 0; mb < MT; mb++)
 #pragma unroll
             for (int nb = 0; nb < NT; nb++)
-                *(v4i *)&red[wave][(16 * mb + l16) * BNP + 16 * nb + 4 * lq] = acc[mb][nb];
+                *(v4i *)&red[buf][wave][(16 * mb + l16) * BNP + 16 * nb + 4 * lq] = acc[mb][nb];
     };
 
     // step i of this wavefront from ring slot `slot`; with groups D is even, so the step's position in its group
@@ -187,9 +192,10 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
                     for (int q = 0; q < QW; q++)
                         if (tid + 256 * q < MAXG * BN) sws[tid + 256 * q] = __uint_as_float(qw[q]);
                 }
-                to_lds();
-                __syncthreads();
                 const int c = i >> 1;
+                const int buf = NRED == 2 ? (c & 1) : 0;
+                to_lds(buf);
+                __syncthreads();
 #pragma unroll
                 for (int w = 0; w < 4; w++) {
                     const int g = 4 * c + w;
@@ -202,8 +208,8 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
                         if (BM % RPP != 0 && tt >= BM) continue;
                         const float xs = sxs[g * BM + tt];
                         const int gsum = sgs[g * BM + tt];
-                        const v4i lo = *(const v4i *)&red[w][tt * BNP + c0];
-                        const v4i hi = *(const v4i *)&red[w][tt * BNP + c0 + 4];
+                        const v4i lo = *(const v4i *)&red[buf][w][tt * BNP + c0];
+                        const v4i hi = *(const v4i *)&red[buf][w][tt * BNP + c0 + 4];
 #pragma unroll
                         for (int j = 0; j < 4; j++) {
                             accf[r][j] = __builtin_fmaf((float)(lo[j] - gsum), xs * wsv[j], accf[r][j]);
@@ -211,7 +217,7 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
                         }
                     }
                 }
-                __syncthreads();
+                if constexpr (NRED == 1) __syncthreads();
             }
         }
     };
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
     for (int i = 0; i < D; i++) compute(i, nsteps - D + i);
 
     if constexpr (!GROUPED) {
-        to_lds();
+        to_lds(0);
         __syncthreads();
         const float wsv[8] = {__int_as_float(wlo[0]), __int_as_float(wlo[1]), __int_as_float(wlo[2]),
                               __int_as_float(wlo[3]), __int_as_float(whi[0]), __int_as_float(whi[1]),
@@ -244,8 +250,8 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
             for (int j = 0; j < 8; j++) S[j] = -gsr[r];
 #pragma unroll
             for (int w = 0; w < 4; w++) {
-                const v4i lo = *(const v4i *)&red[w][tt * BNP + c0];
-                const v4i hi = *(const v4i *)&red[w][tt * BNP + c0 + 4];
+                const v4i lo = *(const v4i *)&red[0][w][tt * BNP + c0];
+                const v4i hi = *(const v4i *)&red[0][w][tt * BNP + c0 + 4];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     S[j] += lo[j];
