@@ -192,13 +192,15 @@ def encoder_setup(synth, n_layers=24):
     return enc, params, sp
 
 
-def encoder_rtfx(torch, synth, enc, dev, reps=5):
+def encoder_rtfx(torch, synth, enc, dev, reps=5, only=None):
     """Device time of encoder forwards from log-mel features (subsampling + 24 layers, each frame count replayed
     from its hipGraph), as RTFx = audio seconds / encoder seconds. Several segments of one length go through one
     batched forward (each segment's output equals its own forward); "sequential_ms" times the same segments one
     forward at a time."""
     out = {}
     for name, t_in, nseg in ENC_WORKLOADS:
+        if only and name != only:
+            continue
         feats = torch.from_numpy(synth.synth_normal(synth.workload_seed(4, t_in & 0xFF), nseg * t_in * 128)
                                  .reshape(nseg, t_in, 128)).to(dev)
 
@@ -408,6 +410,8 @@ def main():
     ap.add_argument("--no-encoder", action="store_true", help="skip the 24-layer encoder RTFx leg")
     ap.add_argument("--encoder-only", action="store_true",
                     help="only the 24-layer encoder RTFx leg (prints its JSON and exits)")
+    ap.add_argument("--encoder-workload", choices=[w[0] for w in ENC_WORKLOADS],
+                    help="with --encoder-only: time this workload alone (for kernel traces)")
     ap.add_argument("--gemm", type=int, nargs=4, metavar=("M", "K", "N", "G"),
                     help="run only this GEMM (Store epilogue), 6 eager launches: for counter collection")
     ap.add_argument("--copy-calib", action="store_true",
@@ -445,7 +449,7 @@ def main():
         return
     if args.encoder_only:
         enc, eparams, esp = encoder_setup(synth)
-        out = {"encoder": encoder_rtfx(torch, synth, enc, dev)}
+        out = {"encoder": encoder_rtfx(torch, synth, enc, dev, only=args.encoder_workload)}
         enc.free()
         if not args.no_cpu:
             out["encoder_cpu"] = cpu_encoder_rtfx(eparams, esp, synth)
