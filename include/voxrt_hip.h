@@ -6,7 +6,8 @@
  *   vx_detect / vx_init               <- kernels::detect (kernels/mod.rs:85-109)
  *   vx_shutdown                       <- (none: drains the device at the end of a session)
  *   vx_tmat_upload_packed             <- TernaryMatrix::from_packed_layout (packed.rs:73-130)
- *   vx_tmat_upload_packed_f32         <- the same with f32 scales (BASELINE config 0's per-channel fp32 scale)
+ *   vx_tmat_upload_packed_f32         <- the same with f32 scales (a per-output-channel fp32 scale, as in the
+ *                                        338 x 1024 x 4096 single-GEMM workload)
  *   vx_tmat_upload_i8                 <- TernaryMatrix::from_i8_rows (packed.rs:164-201)
  *   vx_tmat_free / vx_tmat_info       <- drop / the out, inp, group, ternary fields (packed.rs:48-60)
  *   vx_quantize                       <- QuantAct::quantize_layout (packed.rs:307-436, quantize_group 527-535)
