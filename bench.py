@@ -331,6 +331,29 @@ def cpu_single_core(synth, kernel="vnni"):
             "protocol": f"x86_bench.rs: n=376, 256-row slice, best of 5, {name} restatement"}
 
 
+class Gemv:
+    """One decoder-style GEMV (gemm_single, kernels/mod.rs:285-316): int8 rows [out, 640] with f32 scales in
+    128-column groups, one token, bias; operands as the kernels.rs:271-316 grid draws them, resident on the device."""
+
+    def __init__(self, vx, synth, dev, out, inp=640):
+        import torch
+
+        rng = synth.Lcg(out)
+        rows = (rng.take(out * inp) % 255).astype(np.uint8).view(np.int8).reshape(out, inp)
+        scales = ((rng.take(out * inp // 128) % 100).astype(np.float32) / np.float32(1000.0)
+                  + np.float32(0.001)).astype(np.float32).reshape(out, inp // 128)
+        x = ((rng.take(inp) % 2001).astype(np.float32) / np.float32(100.0) - np.float32(10.0)).reshape(1, inp)
+        self.name, self.vx = f"gemv_{out}x{inp}", vx
+        self.w = vx.TernaryMatrix.from_i8_rows(rows, scales, out, inp, 128)
+        self.x = vx.QuantAct.quantize(torch.from_numpy(x).to(dev), 128)
+        self.bias = torch.from_numpy((rng.take(out) % 100).astype(np.float32)).to(dev)
+        self.y = torch.zeros((1, out), dtype=torch.float32, device=dev)
+        self.bytes = out * inp + out * (inp // 128) * 4 + inp + 8 * (inp // 128) + out * 8
+
+    def run(self):
+        self.vx.gemm_single(self.w, self.x, self.y, self.bias)
+
+
 def attention_us(torch, dev, reps=10):
     """The int8 attention core of one layer alone (8 heads, head_dim 128; q|k|v and the relative rows N(0,1)):
     microseconds per call at T = 338 and 750, and the MAC rate over its 3072*T^2 MACs (Q.K, Q.R band, P.V)."""
@@ -516,6 +539,11 @@ def main():
             details["clip_batch_24_layers"] = clip_batch_tops(torch, vx, synth, dev, eparams)
             details["clip_batch_24_layers_g128"] = clip_batch_tops(torch, vx, synth, dev, eparams, group=128)
             details["attention_core"] = attention_us(torch, dev)
+            gv = [Gemv(vx, synth, dev, out) for out in (8198, 2560)]
+            tg = time_launches(torch, gv, 50)
+            details["gemv_single_token"] = {g.name: {"us": round(tg[g.name] * 1e6, 2),
+                                                    "gb_per_s": round(g.bytes / tg[g.name] / 1e9, 0)} for g in gv}
+            del gv
         if not args.no_cpu:
             ce = cpu_encoder_rtfx(eparams, esp, synth)
             details["encoder_cpu"] = ce
