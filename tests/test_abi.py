@@ -81,3 +81,31 @@ def test_zero_tokens_take_null_pointers():
     assert L.vx_glu_dwconv_silu(None, 0, 256, 9, None, None, None, None) == 0
     assert L.vx_quantize(None, 1, 128, 128, None, None, None, None) == kernels.VX_ERR_INVALID
     assert L.vx_layer_norm(None, 1, 1024, None, None, None, None) == kernels.VX_ERR_INVALID
+
+
+def test_encoder_parameters_are_checked_on_the_host():
+    """Encoder.set_layer / set_subsampling compare every host array with the shape the configuration implies
+    before the C side copies that many bytes (a short array would be over-read)."""
+    from voxrt_amd import encoder as E
+    from voxrt_amd import synth
+
+    p = synth.synth_layer(0, d=256, ff=512, heads=2)
+    enc = E.Encoder(d=256, heads=2, ff=512, n_layers=1, n_mels=32, sub_channels=16)
+    try:
+        for name, edit, msg in [
+            ("o", lambda q: (q[0][:-1], q[1]), "o qweight"),
+            ("ff1_w2", lambda q: (q[0], q[1][:, :-1]), "ff1_w2 scales"),
+        ]:
+            bad = dict(p, linears=dict(p["linears"]))
+            bad["linears"][name] = edit(p["linears"][name])
+            with pytest.raises(ValueError, match=msg):
+                enc.set_layer(0, bad)
+        with pytest.raises(ValueError, match="bias_u"):
+            enc.set_layer(0, dict(p, bias_u=p["bias_u"][:1]))
+        with pytest.raises(ValueError, match="dw"):
+            enc.set_layer(0, dict(p, dw=p["dw"][:, :8]))
+        sp = synth.synth_subsampling(d=256, c=16, n_mels=32)
+        with pytest.raises(ValueError, match="lin_w"):
+            enc.set_subsampling(dict(sp, lin_w=sp["lin_w"][:, :-1]))
+    finally:
+        enc.free()

@@ -572,3 +572,44 @@ def test_zero_tokens_is_a_no_op(dev):
     vx.gemm_rows_range(w, x, y, 0, out, 2, 2)
     torch.cuda.synchronize()
     assert bool((y == 3.0).all())
+
+
+def test_wrappers_refuse_tensors_of_the_wrong_shape(dev):
+    """Every device tensor handed to the C ABI is checked against the shape the call implies (the kernels read or
+    write all of it): a bias, y, group-sum buffer or activation table that is too small raises ValueError before
+    any launch, and y is left untouched."""
+    import torch
+
+    import voxrt_amd as vx
+    from voxrt_amd import encoder as E
+
+    rng = synth.Lcg(78)
+    out, inp, n = 256, 1024, 5
+    qw, s16, _ = synth.ref_random_matrix(rng, out, inp)
+    w = vx.TernaryMatrix.from_packed(qw, s16, out, inp, 128)
+    x = vx.QuantAct.quantize(_t(synth.ref_acts(rng, n, inp), dev), 128)
+    y = torch.full((n, out), 3.0, dtype=torch.float32, device=dev)
+    short = torch.zeros(out - 4, dtype=torch.float32, device=dev)
+    with pytest.raises(ValueError, match="bias"):
+        vx.gemm_ep(w, x, y, short)
+    with pytest.raises(ValueError, match="group_sums"):
+        vx.gemm_ep(w, x, y, None, vx.Epilogue.Store, torch.zeros((8, n, out - 1), dtype=torch.int32, device=dev))
+    with pytest.raises(ValueError, match="y must have shape"):
+        vx.gemm_rows_range(w, x, y[:4], 0, out, 0, 4)
+    with pytest.raises(ValueError, match="bias"):
+        vx.gemm_single(w, x, y, short)
+    bad = vx.QuantAct(x.x, x.scales_t[:, :8], x.gsum_t, n, inp, 128)
+    with pytest.raises(ValueError, match="scales_t"):
+        vx.gemm_ep(w, bad, y)
+    with pytest.raises(ValueError, match="gamma"):
+        vx.QuantAct.quantize_normed(_t(synth.ref_acts(rng, n, inp), dev), short, short, 128)
+    with pytest.raises(ValueError, match="rel_k"):
+        E.attention_core(torch.zeros((9, 3 * 256), device=dev), torch.zeros((16, 256), device=dev), 2,
+                         torch.zeros((2, 128), device=dev), torch.zeros((2, 128), device=dev))
+    enc = E.Encoder(d=256, heads=2, ff=512, n_layers=1)
+    with pytest.raises(ValueError, match="x must have shape"):
+        enc.forward(torch.zeros((9, 255), device=dev))
+    enc.free()
+    torch.cuda.synchronize()
+    assert bool((y == 3.0).all())
+    w.free()

@@ -125,6 +125,24 @@ def test_qkv_is_stacked_in_q_k_v_order(mdir):
         M.packed_linear(m, ["encoder.layers.0.self_attn.q_proj", "encoder.layers.0.feed_forward1.linear2"])
 
 
+def test_module_group_must_match_the_encoder_group(mdir, tmp_path):
+    """Each linear's own group_size (ternary_linear.rs:70-76) is checked against the encoder's group before any
+    scale table reaches the device: a module declaring 64-column groups is refused, whatever its tensors hold."""
+    path = mdir[0]
+    m = M.ModelFile(path)
+    assert M.layer_params(m, 0, 128)["linears"]["o"][1].shape == (256, 2)
+
+    def edit(tj):
+        for mod in tj["quantized_modules"]:
+            if mod["name"] == "encoder.layers.1.self_attn.o_proj":
+                mod["group_size"] = 64
+
+    bad = M.ModelFile(_rewrite(path, str(tmp_path / "grp"), edit_ternary=edit))
+    M.layer_params(bad, 0, 128)
+    with pytest.raises(M.FormatError, match="group_size 64 differs"):
+        M.layer_params(bad, 1, 128)
+
+
 def test_subsampling_params_against_torch_on_the_file_layout(mdir, orc):
     """The loader's subsampling (taps to [k*k, C], the final linear's columns to channels-last) through the oracle
     equals torch float64 on the file's own tensors: NCHW convolutions and the HF flatten order c*F + f."""

@@ -28,10 +28,16 @@ LAYER_LINEARS = ("ff1_w1", "ff1_w2", "qkv", "o", "pos", "pw1", "pw2", "ff2_w1", 
 LAYER_NORMS = ("ff1", "attn", "conv", "ff2", "out")
 
 
-def _f32(t, name):
+def _f32(t, name, shape=None):
     import torch
 
-    return K._dev_ptr(t, torch.float32, name)
+    return K._dev_ptr(t, torch.float32, name, shape)
+
+
+def _dims(t, nd, name):
+    if t.dim() != nd:
+        raise ValueError(f"{name} must have {nd} dimensions, not {t.dim()}")
+    return tuple(int(v) for v in t.shape)
 
 
 class TernaryLinear:
@@ -85,10 +91,10 @@ class TernaryLinear:
 def layer_norm(x, gamma, beta, y=None):
     import torch
 
-    n, d = x.shape
+    n, d = _dims(x, 2, "x")
     y = torch.empty_like(x) if y is None else y
-    check(lib().vx_layer_norm(_f32(x, "x"), n, d, _f32(gamma, "gamma"), _f32(beta, "beta"), _f32(y, "y"),
-                              K._stream()))
+    check(lib().vx_layer_norm(_f32(x, "x"), n, d, _f32(gamma, "gamma", (d,)), _f32(beta, "beta", (d,)),
+                              _f32(y, "y", (n, d)), K._stream()))
     return y
 
 
@@ -107,11 +113,11 @@ def glu_dwconv_silu(g, w_t, bias, out=None):
     """g [t, 2d] -> silu(dwconv_bn(glu(g))) [t, d]; w_t [k, d], bias [d] from fold_bn (device tensors)."""
     import torch
 
-    t, d2 = g.shape
-    k = w_t.shape[0]
-    out = torch.empty((t, d2 // 2), dtype=torch.float32, device=g.device) if out is None else out
-    check(lib().vx_glu_dwconv_silu(_f32(g, "g"), t, d2 // 2, k, _f32(w_t, "w_t"), _f32(bias, "bias"),
-                                   _f32(out, "out"), K._stream()))
+    t, d2 = _dims(g, 2, "g")
+    d, k = d2 // 2, _dims(w_t, 2, "w_t")[0]
+    out = torch.empty((t, d), dtype=torch.float32, device=g.device) if out is None else out
+    check(lib().vx_glu_dwconv_silu(_f32(g, "g", (t, 2 * d)), t, d, k, _f32(w_t, "w_t", (k, d)),
+                                   _f32(bias, "bias", (d,)), _f32(out, "out", (t, d)), K._stream()))
     return out
 
 
@@ -120,12 +126,15 @@ def glu_dwconv_silu_quantize(g, w_t, bias, group=128):
     128-channel groups."""
     import torch
 
-    t, d2 = g.shape
-    d, k = d2 // 2, w_t.shape[0]
+    t, d2 = _dims(g, 2, "g")
+    d, k = d2 // 2, _dims(w_t, 2, "w_t")[0]
+    if group <= 0 or d % group:
+        raise ValueError("d must be a multiple of group")
     q = torch.empty((t, d), dtype=torch.int8, device=g.device)
     s = torch.empty((d // group, K.npad(t)), dtype=torch.float32, device=g.device)
     gs = torch.empty((d // group, K.npad(t)), dtype=torch.int32, device=g.device)
-    check(lib().vx_glu_dwconv_silu_quantize(_f32(g, "g"), t, d, k, _f32(w_t, "w_t"), _f32(bias, "bias"), group,
+    check(lib().vx_glu_dwconv_silu_quantize(_f32(g, "g", (t, 2 * d)), t, d, k, _f32(w_t, "w_t", (k, d)),
+                                            _f32(bias, "bias", (d,)), group,
                                             K._dev_ptr(q, torch.int8, "q"), _f32(s, "scales_t"),
                                             K._dev_ptr(gs, torch.int32, "gsum_t"), K._stream()))
     return K.QuantAct(q, s, gs, t, d, group)
@@ -134,11 +143,11 @@ def glu_dwconv_silu_quantize(g, w_t, bias, group=128):
 def linear_f32(x, w, b=None, relu=False, y=None):
     import torch
 
-    n, in_f = x.shape
-    out_f = w.shape[0]
+    n, in_f = _dims(x, 2, "x")
+    out_f = _dims(w, 2, "w")[0]
     y = torch.empty((n, out_f), dtype=torch.float32, device=x.device) if y is None else y
-    check(lib().vx_linear_f32(_f32(x, "x"), n, in_f, _f32(w, "w"), _f32(b, "b"), out_f, _f32(y, "y"), int(relu),
-                              K._stream()))
+    check(lib().vx_linear_f32(_f32(x, "x"), n, in_f, _f32(w, "w", (out_f, in_f)), _f32(b, "b", (out_f,)), out_f,
+                              _f32(y, "y", (n, out_f)), int(relu), K._stream()))
     return y
 
 
@@ -153,22 +162,35 @@ def attention_ws_bytes(t: int, d: int, heads: int) -> int:
     return int(lib().vx_attention_ws_bytes(t, d, heads))
 
 
+def _attention_ws(t, d, heads, ws, device):
+    """The attention core's device workspace: a new one, or the caller's uint8 tensor if it is large enough."""
+    import torch
+
+    nb = attention_ws_bytes(t, d, heads)
+    if nb < 0:
+        raise ValueError("attention: d must be heads * 128")
+    if ws is None:
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=device)
+    K._dev_ptr(ws, torch.uint8, "ws")
+    if ws.numel() < nb:
+        raise ValueError(f"ws must hold at least {nb} bytes")
+    return C.c_void_p(ws.data_ptr())
+
+
 def attention_core(qkv, rel_k, heads, bias_u, bias_v, ctx=None, ws=None):
     """The int8 attention core of one layer (attn_core_int8, encoder.rs:317-534): qkv [t, 3d], rel_k [2t-1, d],
     bias_u / bias_v [heads, 128] -> ctx [t, d]."""
     import torch
 
-    t, d3 = qkv.shape
+    t, d3 = _dims(qkv, 2, "qkv")
     d = d3 // 3
     ctx = torch.empty((t, d), dtype=torch.float32, device=qkv.device) if ctx is None else ctx
-    nb = attention_ws_bytes(t, d, heads)
-    if nb < 0:
-        raise ValueError("attention: d must be heads * 128")
-    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=qkv.device) if ws is None else ws
+    ws = _attention_ws(t, d, heads, ws, qkv.device)
     scaling = float(np.float32(1.0) / np.sqrt(np.float32(d // heads)))
-    check(lib().vx_attention_core(_f32(qkv, "qkv"), _f32(rel_k, "rel_k"), t, d, heads, _f32(bias_u, "bias_u"),
-                                  _f32(bias_v, "bias_v"), scaling, C.c_void_p(ws.data_ptr()), _f32(ctx, "ctx"),
-                                  K._stream()))
+    dh = d // heads
+    check(lib().vx_attention_core(_f32(qkv, "qkv", (t, 3 * d)), _f32(rel_k, "rel_k", (2 * t - 1, d)), t, d, heads,
+                                  _f32(bias_u, "bias_u", (heads, dh)), _f32(bias_v, "bias_v", (heads, dh)), scaling,
+                                  ws, _f32(ctx, "ctx", (t, d)), K._stream()))
     return ctx
 
 
@@ -177,19 +199,19 @@ def attention_core_quantize(qkv, rel_k, heads, bias_u, bias_v, group=128, ws=Non
     groups, one per head."""
     import torch
 
-    t, d3 = qkv.shape
+    t, d3 = _dims(qkv, 2, "qkv")
     d = d3 // 3
-    nb = attention_ws_bytes(t, d, heads)
-    if nb < 0:
-        raise ValueError("attention: d must be heads * 128")
-    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=qkv.device) if ws is None else ws
+    if group <= 0 or d % group:
+        raise ValueError("d must be a multiple of group")
+    ws = _attention_ws(t, d, heads, ws, qkv.device)
+    dh = d // heads
     scaling = float(np.float32(1.0) / np.sqrt(np.float32(d // heads)))
     q = torch.empty((t, d), dtype=torch.int8, device=qkv.device)
     s = torch.empty((d // group, K.npad(t)), dtype=torch.float32, device=qkv.device)
     gs = torch.empty((d // group, K.npad(t)), dtype=torch.int32, device=qkv.device)
-    check(lib().vx_attention_core_quantize(_f32(qkv, "qkv"), _f32(rel_k, "rel_k"), t, d, heads,
-                                           _f32(bias_u, "bias_u"), _f32(bias_v, "bias_v"), scaling,
-                                           C.c_void_p(ws.data_ptr()), group, K._dev_ptr(q, torch.int8, "q"),
+    check(lib().vx_attention_core_quantize(_f32(qkv, "qkv", (t, 3 * d)), _f32(rel_k, "rel_k", (2 * t - 1, d)), t,
+                                           d, heads, _f32(bias_u, "bias_u", (heads, dh)),
+                                           _f32(bias_v, "bias_v", (heads, dh)), scaling, ws, group, K._dev_ptr(q, torch.int8, "q"),
                                            _f32(s, "scales_t"), K._dev_ptr(gs, torch.int32, "gsum_t"), K._stream()))
     return K.QuantAct(q, s, gs, t, d, group)
 
@@ -216,7 +238,9 @@ class Subsampling:
     def forward(self, feats):
         import torch
 
-        t, nm = feats.shape
+        t, nm = _dims(feats, 2, "feats")
+        if nm != self.n_mels:
+            raise ValueError(f"feats must have {self.n_mels} mel columns")
         t3 = self.out_frames(t)
         out = torch.empty((t3, self.d), dtype=torch.float32, device=feats.device)
         scratch = torch.empty(int(lib().vx_subsampling_scratch_floats(t, nm, self.c, self.k, self.s)),
@@ -253,37 +277,55 @@ class Encoder:
         check(lib().vx_encoder_create(C.byref(cfg), C.byref(h)))
         self._h = h
         self.d, self.heads, self.ff, self.kconv, self.group, self.n_layers = d, heads, ff, kconv, group, n_layers
-        self.n_mels, self.sub_kernel, self.sub_stride = n_mels, sub_kernel, sub_stride
+        self.n_mels, self.sub_channels, self.sub_kernel, self.sub_stride = n_mels, sub_channels, sub_kernel, sub_stride
 
     def set_layer(self, i: int, p: dict) -> None:
         """p: {"linears": {name: (qweight, scales_f16)}, "norms": {name: (g, b)}, "bias_u", "bias_v", "dw" [d, k],
         "bn": {"gamma", "beta", "mean", "var"}} as synth.synth_layer produces (the model file's tensors)."""
         keep = []
 
-        def ptr(a, dtype):
-            a = np.ascontiguousarray(np.asarray(a).view(dtype) if np.asarray(a).dtype != dtype and dtype == np.uint16
-                                     else a, dtype)
+        def ptr(a, dtype, shape, name):
+            a = np.asarray(a)
+            if dtype == np.uint16 and a.dtype == np.float16:
+                a = a.view(np.uint16)
+            a = np.ascontiguousarray(a, dtype)
+            if a.shape != tuple(shape):
+                raise ValueError(f"layer {i}: {name} must have shape {tuple(shape)}, not {a.shape}")
             keep.append(a)
             return a.ctypes.data
 
+        d, ff, G = self.d, self.ff, self.group
+        dims = {"ff1_w1": (ff, d), "ff1_w2": (d, ff), "qkv": (3 * d, d), "o": (d, d), "pos": (d, d),
+                "pw1": (2 * d, d), "pw2": (d, d), "ff2_w1": (ff, d), "ff2_w2": (d, ff)}
         lp = _LayerParams()
         for i_, n in enumerate(LAYER_LINEARS):
             q, s = p["linears"][n]
-            lp.qweight[i_] = ptr(q, np.uint8)
-            lp.scales_f16[i_] = ptr(s, np.uint16)
+            out, inp = dims[n]
+            lp.qweight[i_] = ptr(q, np.uint8, (out, (inp + 4) // 5), f"{n} qweight")
+            lp.scales_f16[i_] = ptr(s, np.uint16, (out, inp // G), f"{n} scales")
         for i_, n in enumerate(LAYER_NORMS):
             g, b = p["norms"][n]
-            lp.ln_gamma[i_] = ptr(g, np.float32)
-            lp.ln_beta[i_] = ptr(b, np.float32)
-        lp.bias_u, lp.bias_v = ptr(p["bias_u"], np.float32), ptr(p["bias_v"], np.float32)
-        lp.dw = ptr(p["dw"], np.float32)
+            lp.ln_gamma[i_] = ptr(g, np.float32, (d,), f"norm {n} weight")
+            lp.ln_beta[i_] = ptr(b, np.float32, (d,), f"norm {n} bias")
+        hd = (self.heads, d // self.heads)
+        lp.bias_u, lp.bias_v = ptr(p["bias_u"], np.float32, hd, "bias_u"), ptr(p["bias_v"], np.float32, hd, "bias_v")
+        lp.dw = ptr(p["dw"], np.float32, (d, self.kconv), "dw")
         bn = p["bn"]
-        lp.bn_gamma, lp.bn_beta = ptr(bn["gamma"], np.float32), ptr(bn["beta"], np.float32)
-        lp.bn_mean, lp.bn_var = ptr(bn["mean"], np.float32), ptr(bn["var"], np.float32)
+        lp.bn_gamma, lp.bn_beta = ptr(bn["gamma"], np.float32, (d,), "bn gamma"), ptr(bn["beta"], np.float32, (d,), "bn beta")
+        lp.bn_mean, lp.bn_var = ptr(bn["mean"], np.float32, (d,), "bn mean"), ptr(bn["var"], np.float32, (d,), "bn var")
         check(lib().vx_encoder_set_layer(self._h, i, C.byref(lp)))
 
     def set_subsampling(self, params: dict) -> None:
         arrs = {k: np.ascontiguousarray(params[k], np.float32) for k in SUB_KEYS}
+        k, c, d = self.sub_kernel, self.sub_channels, self.d
+        f3 = self.n_mels
+        for _ in range(3):
+            f3 = (f3 + 2 * ((k - 1) // 2) - k) // self.sub_stride + 1
+        want = {"conv0_w": (k * k, c), "conv0_b": (c,), "dw_w": (2, k * k, c), "dw_b": (2, c), "pw_w": (2, c, c),
+                "pw_b": (2, c), "lin_w": (d, f3 * c), "lin_b": (d,)}
+        for key, shape in want.items():
+            if arrs[key].shape != shape:
+                raise ValueError(f"subsampling {key} must have shape {shape}, not {arrs[key].shape}")
         sp = _SubParams(*[arrs[k].ctypes.data for k in SUB_KEYS])
         check(lib().vx_encoder_set_subsampling(self._h, C.byref(sp)))
 
@@ -294,9 +336,10 @@ class Encoder:
         """The layer stack on x [t, d] (the subsampling output); returns out [t, d]."""
         import torch
 
-        t = x.shape[0]
+        t, _ = _dims(x, 2, "x")
         out = torch.empty_like(x) if out is None else out
-        check(lib().vx_encoder_forward(self._h, _f32(x, "x"), _f32(out, "out"), t, K._stream()))
+        check(lib().vx_encoder_forward(self._h, _f32(x, "x", (t, self.d)), _f32(out, "out", (t, self.d)), t,
+                                       K._stream()))
         return out
 
     def out_frames(self, t_in: int) -> int:
@@ -306,12 +349,12 @@ class Encoder:
         """Subsampling + layers: feats [t_in, n_mels] -> [t_out, d]."""
         import torch
 
-        t_in = feats.shape[0]
+        t_in, _ = _dims(feats, 2, "feats")
         t3 = self.out_frames(t_in)
         out = torch.empty((t3, self.d), dtype=torch.float32, device=feats.device) if out is None else out
         got = C.c_int64()
-        check(lib().vx_encoder_forward_feats(self._h, _f32(feats, "feats"), t_in, _f32(out, "out"), C.byref(got),
-                                             K._stream()))
+        check(lib().vx_encoder_forward_feats(self._h, _f32(feats, "feats", (t_in, self.n_mels)), t_in,
+                                             _f32(out, "out", (t3, self.d)), C.byref(got), K._stream()))
         return out
 
     def forward_batch(self, x, out=None):
@@ -319,9 +362,10 @@ class Encoder:
         segment's output equals forward() of that segment alone, bit for bit."""
         import torch
 
-        nseg, t = x.shape[0], x.shape[1]
+        nseg, t, _ = _dims(x, 3, "x")
         out = torch.empty_like(x) if out is None else out
-        check(lib().vx_encoder_forward_batch(self._h, _f32(x, "x"), _f32(out, "out"), nseg, t, K._stream()))
+        check(lib().vx_encoder_forward_batch(self._h, _f32(x, "x", (nseg, t, self.d)),
+                                             _f32(out, "out", (nseg, t, self.d)), nseg, t, K._stream()))
         return out
 
     def forward_feats_batch(self, feats, out=None):
@@ -329,12 +373,13 @@ class Encoder:
         each segment equal to forward_feats() of that segment alone."""
         import torch
 
-        nseg, t_in = feats.shape[0], feats.shape[1]
+        nseg, t_in, _ = _dims(feats, 3, "feats")
         t3 = self.out_frames(t_in)
         out = torch.empty((nseg, t3, self.d), dtype=torch.float32, device=feats.device) if out is None else out
         got = C.c_int64()
-        check(lib().vx_encoder_forward_feats_batch(self._h, _f32(feats, "feats"), nseg, t_in, _f32(out, "out"),
-                                                   C.byref(got), K._stream()))
+        check(lib().vx_encoder_forward_feats_batch(self._h, _f32(feats, "feats", (nseg, t_in, self.n_mels)), nseg,
+                                                   t_in, _f32(out, "out", (nseg, t3, self.d)), C.byref(got),
+                                                   K._stream()))
         return out
 
     def free(self) -> None:

@@ -151,7 +151,9 @@ def _stream(stream=None):
     return C.c_void_p(s.cuda_stream)
 
 
-def _dev_ptr(t, dtype, name):
+def _dev_ptr(t, dtype, name, shape=None):
+    """Device address of a contiguous tensor of `dtype`; with `shape`, the tensor must have exactly that shape (the
+    kernels read and write every element of the shape the call implies, so a smaller tensor would be overrun)."""
     import torch
 
     if t is None:
@@ -160,7 +162,19 @@ def _dev_ptr(t, dtype, name):
         raise TypeError(f"{name} must be a device tensor")
     if t.dtype != dtype or not t.is_contiguous():
         raise TypeError(f"{name} must be a contiguous {dtype} tensor")
+    if shape is not None and tuple(t.shape) != tuple(int(v) for v in shape):
+        raise ValueError(f"{name} must have shape {tuple(int(v) for v in shape)}, not {tuple(t.shape)}")
     return C.c_void_p(t.data_ptr())
+
+
+def _act_ptrs(x: "QuantAct"):
+    """The three device operands of a QuantAct, each checked against its n, inp and group."""
+    import torch
+
+    ng = x.inp // x.group
+    return (_dev_ptr(x.x, torch.int8, "x", (x.n, x.inp)),
+            _dev_ptr(x.scales_t, torch.float32, "scales_t", (ng, npad(x.n))),
+            _dev_ptr(x.gsum_t, torch.int32, "gsum_t", (ng, npad(x.n))))
 
 
 class TernaryMatrix:
@@ -249,6 +263,8 @@ class QuantAct:
         """QuantAct::from_rows over LayerNorm rows (TernaryLinear::prepare_normed, ternary_linear.rs:132-155)."""
         import torch
 
+        if x.dim() != 2:
+            raise ValueError("x must be [n, inp]")
         n, inp = x.shape
         if group <= 0 or inp % group:
             raise ValueError("inp must be a multiple of group")
@@ -256,7 +272,8 @@ class QuantAct:
         s = torch.empty((inp // group, npad(n)), dtype=torch.float32, device=x.device)
         g = torch.empty((inp // group, npad(n)), dtype=torch.int32, device=x.device)
         check(lib().vx_quantize_normed(_dev_ptr(x, torch.float32, "x"), n, inp, group,
-                                       _dev_ptr(gamma, torch.float32, "gamma"), _dev_ptr(beta, torch.float32, "beta"),
+                                       _dev_ptr(gamma, torch.float32, "gamma", (inp,)),
+                                       _dev_ptr(beta, torch.float32, "beta", (inp,)),
                                        _dev_ptr(q, torch.int8, "q"), _dev_ptr(s, torch.float32, "scales_t"),
                                        _dev_ptr(g, torch.int32, "gsum_t"), _stream(stream)))
         return cls(q, s, g, n, inp, group)
@@ -266,6 +283,8 @@ class QuantAct:
         """QuantAct::quantize_layout (packed.rs:307-436) on a float32 device tensor [n, inp]."""
         import torch
 
+        if x.dim() != 2:
+            raise ValueError("x must be [n, inp]")
         n, inp = x.shape
         if group <= 0 or inp % group:
             raise ValueError("inp must be a multiple of group")
@@ -286,12 +305,10 @@ def gemm_ep(w: TernaryMatrix, x: QuantAct, y, bias=None, ep: Epilogue = Epilogue
 
     if x.inp != w.inp or x.group != w.group:
         raise ValueError("activation and weight shapes or groups differ")
-    if tuple(y.shape) != (x.n, w.out):
-        raise ValueError("y must be [n, out]")
-    check(lib().vx_gemm_ep(w._h, _dev_ptr(x.x, torch.int8, "x"), _dev_ptr(x.scales_t, torch.float32, "scales_t"),
-                           _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), x.n, _dev_ptr(y, torch.float32, "y"),
-                           _dev_ptr(bias, torch.float32, "bias"), ep.kind, ep.alpha,
-                           _dev_ptr(group_sums, torch.int32, "group_sums"), _stream(stream)))
+    check(lib().vx_gemm_ep(w._h, *_act_ptrs(x), x.n, _dev_ptr(y, torch.float32, "y", (x.n, w.out)),
+                           _dev_ptr(bias, torch.float32, "bias", (w.out,)), ep.kind, ep.alpha,
+                           _dev_ptr(group_sums, torch.int32, "group_sums", (w.groups(), x.n, w.out)),
+                           _stream(stream)))
 
 
 def gemm_ep_quantize(w: TernaryMatrix, x: QuantAct, bias=None, ep: Epilogue = Epilogue.Silu, group: int = 128,
@@ -315,9 +332,8 @@ def gemm_ep_quantize(w: TernaryMatrix, x: QuantAct, bias=None, ep: Epilogue = Ep
     q = torch.empty((n, w.out), dtype=torch.int8, device=dev)
     s = torch.empty((w.out // group, npad(n)), dtype=torch.float32, device=dev)
     g = torch.empty((w.out // group, npad(n)), dtype=torch.int32, device=dev)
-    check(lib().vx_gemm_ep_quantize(w._h, _dev_ptr(x.x, torch.int8, "x"), _dev_ptr(x.scales_t, torch.float32, "scales_t"),
-                                    _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), n, _dev_ptr(y_tmp, torch.float32, "y_tmp"),
-                                    _dev_ptr(bias, torch.float32, "bias"), ep.kind, group,
+    check(lib().vx_gemm_ep_quantize(w._h, *_act_ptrs(x), n, _dev_ptr(y_tmp, torch.float32, "y_tmp", (n, w.out)),
+                                    _dev_ptr(bias, torch.float32, "bias", (w.out,)), ep.kind, group,
                                     _dev_ptr(q, torch.int8, "q"), _dev_ptr(s, torch.float32, "scales_t"),
                                     _dev_ptr(g, torch.int32, "gsum_t"), _stream(stream)))
     return QuantAct(q, s, g, n, w.out, group)
@@ -334,10 +350,8 @@ def gemm_rows_range(w: TernaryMatrix, x: QuantAct, y, r0: int, r1: int, t0: int,
 
     if x.inp != w.inp or x.group != w.group:
         raise ValueError("activation and weight shapes or groups differ")
-    check(lib().vx_gemm_rows_range(w._h, _dev_ptr(x.x, torch.int8, "x"),
-                                   _dev_ptr(x.scales_t, torch.float32, "scales_t"),
-                                   _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), x.n, _dev_ptr(y, torch.float32, "y"), r0,
-                                   r1, t0, t1, ep.kind, ep.alpha, _stream(stream)))
+    check(lib().vx_gemm_rows_range(w._h, *_act_ptrs(x), x.n, _dev_ptr(y, torch.float32, "y", (x.n, w.out)), r0, r1,
+                                   t0, t1, ep.kind, ep.alpha, _stream(stream)))
 
 
 def gemm_single(w: TernaryMatrix, x: QuantAct, y, bias=None, stream=None) -> None:
@@ -346,9 +360,8 @@ def gemm_single(w: TernaryMatrix, x: QuantAct, y, bias=None, stream=None) -> Non
 
     if x.inp != w.inp or x.group != w.group:
         raise ValueError("activation and weight shapes or groups differ")
-    check(lib().vx_gemm_single(w._h, _dev_ptr(x.x, torch.int8, "x"), _dev_ptr(x.scales_t, torch.float32, "scales_t"),
-                               _dev_ptr(x.gsum_t, torch.int32, "gsum_t"), x.n, _dev_ptr(y, torch.float32, "y"),
-                               _dev_ptr(bias, torch.float32, "bias"), _stream(stream)))
+    check(lib().vx_gemm_single(w._h, *_act_ptrs(x), x.n, _dev_ptr(y, torch.float32, "y", (x.n, w.out)),
+                               _dev_ptr(bias, torch.float32, "bias", (w.out,)), _stream(stream)))
 
 
 def check_activations() -> tuple:

@@ -155,13 +155,17 @@ class ModelFile:
         return problems + extra
 
 
-def packed_linear(m: ModelFile, names) -> tuple:
+def packed_linear(m: ModelFile, names, group: int | None = None) -> tuple:
     """TernaryLinear::load / load_stacked (ternary_linear.rs:59-98): the packed rows and f16 scales of one module,
     or of several with the same input stacked along the output dimension (q | k | v), in the model file's own
-    layout: (qweight uint8 [out, ceil(in/5)], scales as uint16 bits [out, in/group])."""
-    qs, ss, inp, group = [], [], None, None
+    layout: (qweight uint8 [out, ceil(in/5)], scales as uint16 bits [out, in/group]). Each module's own group_size
+    (ternary_linear.rs:70-76) is read from ternary.json; when `group` is given every module must use it (the GPU
+    encoder holds one group for all its linears)."""
+    qs, ss, inp = [], [], None
     for name in names:
         q = m.module(name)
+        if group is not None and q["group_size"] != group:
+            raise FormatError(f"{name}: group_size {q['group_size']} differs from the encoder's group {group}")
         if inp is not None and (q["in_features"] != inp or q["group_size"] != group):
             raise FormatError(f"{name}: cannot stack, shapes differ")
         if q["has_bias"]:
@@ -177,7 +181,7 @@ def packed_linear(m: ModelFile, names) -> tuple:
     return np.ascontiguousarray(np.concatenate(qs)), np.ascontiguousarray(np.concatenate(ss))
 
 
-def layer_params(m: ModelFile, i: int) -> dict:
+def layer_params(m: ModelFile, i: int, group: int | None = None) -> dict:
     """ConformerLayer::load (encoder.rs:677-692) with FeedForward / Attention / ConvModule::load
     (encoder.rs:70-76,108-134,546-574): the parameters of layer i in the form Encoder.set_layer takes (the BatchNorm
     fold into the depthwise taps happens at upload, as ConvModule::load does)."""
@@ -194,7 +198,7 @@ def layer_params(m: ModelFile, i: int) -> dict:
     norms = {"ff1": "norm_feed_forward1", "attn": "norm_self_att", "conv": "norm_conv", "ff2": "norm_feed_forward2",
              "out": "norm_out"}
     return {
-        "linears": {n: packed_linear(m, names) for n, names in lin.items()},
+        "linears": {n: packed_linear(m, names, group) for n, names in lin.items()},
         "norms": {n: (m.load_f32(f"{p}.{v}.weight", [d]), m.load_f32(f"{p}.{v}.bias", [d])) for n, v in norms.items()},
         "bias_u": m.load_f32(f"{p}.self_attn.bias_u", [heads, d // heads]),
         "bias_v": m.load_f32(f"{p}.self_attn.bias_v", [heads, d // heads]),
@@ -243,7 +247,7 @@ def load_encoder(m: ModelFile):
                   sub_stride=e["subsampling_conv_stride"])
     try:
         for i in range(e["num_hidden_layers"]):
-            enc.set_layer(i, layer_params(m, i))
+            enc.set_layer(i, layer_params(m, i, group))
         enc.set_subsampling(subsampling_params(m))
     except Exception:
         enc.free()
