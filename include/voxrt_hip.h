@@ -25,6 +25,8 @@
  *   vx_attention_core*                <- attn_core_int8 (encoder.rs:317-534)
  *   vx_encoder_*                      <- GpuEncoder::{load, forward, forward_feats} (metal/mod.rs:446-603) on the
  *                                        CPU int8 Encoder's operation order (encoder.rs:706-857)
+ *   vx_encoder_set_profiling / _take_profile <- VOXRT_PROFILE's per-sublayer Profile (encoder.rs:645-653,823-854)
+ *   vx_encoder_memory                 <- (none: the workspace size and graph count, for hosts that bound memory)
  *   vx_last_error                     <- voxrt_last_error (crates/voxrt-ffi/src/lib.rs:61-74)
  *   vx_check_activations              <- (none: device self-check of exp_poly/silu_fast/sigmoid_fast)
  *
@@ -236,11 +238,34 @@ vx_status vx_encoder_create(const vx_encoder_config *cfg, vx_encoder **enc);
 /* Upload layer `layer`'s weights (every layer must be set before a forward). */
 vx_status vx_encoder_set_layer(vx_encoder *enc, int64_t layer, const vx_layer_params *p);
 vx_status vx_encoder_set_subsampling(vx_encoder *enc, const vx_subsampling_params *p);
-/* 1 (default): each frame count's layer stack is captured once into a hipGraph and replayed on a non-NULL stream;
- * 0: kernels are launched one by one. */
+/* 1 (default): the layer stack of each (frames, segments) pair is captured once into a hipGraph (on a private stream:
+ * nothing runs during the capture) and launched on the caller's stream, NULL included; the 8 most recently used
+ * graphs are kept. 0: kernels are launched one by one. */
 vx_status vx_encoder_use_graphs(vx_encoder *enc, int on);
+
+/* Wall-clock device time per sublayer type, summed over layers and over the forwards since the last take
+ * (encoder.rs:645-653 Profile; attn includes attn_core). */
+typedef struct vx_encoder_profile {
+    double total_ms, subsampling_ms, ff_ms, attn_ms, attn_core_ms, conv_ms, norm_ms;
+    int64_t forwards;
+} vx_encoder_profile;
+/* 1: every forward launches its kernels one by one with device events between the sublayers and waits for them
+ * (a timing mode, as VOXRT_PROFILE=1 is for the reference's encoder); 0 (default): off. */
+vx_status vx_encoder_set_profiling(vx_encoder *enc, int on);
+/* The sums since the previous take (then reset). */
+vx_status vx_encoder_take_profile(vx_encoder *enc, vx_encoder_profile *out);
+/* Device bytes of the encoder's workspace (weights not counted) and the number of graphs kept. */
+vx_status vx_encoder_memory(vx_encoder *enc, int64_t *workspace_bytes, int64_t *graphs);
+
+/* Memory and concurrency of the forward calls (GpuEncoder's Mutex-guarded workspace, metal/mod.rs:449-460,641-645):
+ * one device workspace serves every frame count and segment count; it grows to 1.25x a call's need when a call needs
+ * more (after the device has finished the previous forward) and never shrinks. Calls on one encoder may come from
+ * any threads and streams: they are serialized on the host, and each forward's work waits on the device for the
+ * previous forward's, so they never share the workspace at the same time. The encoder belongs to the device that
+ * was current at vx_encoder_create (or at its first weight upload, when none was then). */
+
 /* The layer stack (GpuEncoder::forward): x [t, d] (device, the subsampling output) -> out [t, d] (may alias x);
- * 1 <= t <= 1024. A workspace is kept per distinct t. Calls on one encoder must not overlap. */
+ * 1 <= t <= 1024. */
 vx_status vx_encoder_forward(vx_encoder *enc, const float *x, float *out, int64_t t, void *stream);
 /* Subsampling + layers (GpuEncoder::forward_feats): feats [t_in, n_mels] (device) -> out [t_out, d] (device, sized
  * for vx_subsampling_frames(t_in, sub_kernel, sub_stride) rows). */
@@ -251,7 +276,7 @@ vx_status vx_encoder_forward_feats(vx_encoder *enc, const float *feats, int64_t 
  * runs over all nseg * t rows at once, while the depthwise convolution, the attention and the subsampling stay
  * inside each segment. The reference encodes one VAD segment per call (Transcriber::transcribe_long,
  * transcriber.rs:356-386); these entry points have no counterpart there and serve callers that hold several
- * segments of one length at once. nseg * t <= 65535; a workspace is kept per distinct (t, nseg). */
+ * segments of one length at once. nseg * t <= 65535. */
 vx_status vx_encoder_forward_batch(vx_encoder *enc, const float *x, float *out, int64_t nseg, int64_t t, void *stream);
 vx_status vx_encoder_forward_feats_batch(vx_encoder *enc, const float *feats, int64_t nseg, int64_t t_in, float *out,
                                          int64_t *t_out, void *stream);

@@ -361,3 +361,96 @@ def test_encoder_from_model_directory(dev, orc, tmp_path):
     for i in range(2):
         x = orc.conformer_layer(x, pos, _oracle_layer(orc, M.layer_params(m, i)), heads=8)
     _bits_equal(got, x, "encoder from a model directory")
+
+
+def _small_encoder(n_layers=2, d=256, heads=2, ff=1024):
+    from voxrt_amd import encoder as E
+
+    params = [synth.synth_layer(40 + i, d=d, ff=ff, heads=heads) for i in range(n_layers)]
+    enc = E.Encoder(d=d, heads=heads, ff=ff, n_layers=n_layers)
+    for i, p in enumerate(params):
+        enc.set_layer(i, p)
+    return enc, params
+
+
+def _oracle_stack(orc, x, params, heads):
+    pos = orc.rel_pos_table(x.shape[0], x.shape[1])
+    for p in params:
+        x = orc.conformer_layer(x, pos, _oracle_layer(orc, p), heads=heads)
+    return x
+
+
+def test_encoder_workspace_is_bounded_over_many_lengths(dev, orc):
+    """20 distinct frame counts in a row (VAD-like segment lengths, the longest fifth): one workspace serves them
+    all. It stops growing once the longest has run, at most 8 graphs are kept, and every output equals the oracle
+    bit for bit (GpuEncoder's single growing workspace, metal/mod.rs:449-460,641-645)."""
+    enc, params = _small_encoder()
+    lengths = [25, 188, 60, 125, 750, 33, 97, 140, 301, 64, 1, 17, 480, 199, 2, 77, 256, 49, 600, 333]
+    assert len(set(lengths)) == 20
+    sizes = []
+    for i, t in enumerate(lengths):
+        x = _x(300 + t, t, 256)
+        got = enc.forward(_t(x, dev)).cpu().numpy()
+        _bits_equal(got, _oracle_stack(orc, x, params, 2), f"t={t}")
+        ws, graphs = enc.memory()
+        sizes.append(ws)
+        assert graphs <= 8, graphs
+    top = lengths.index(750)
+    assert all(s == sizes[top] for s in sizes[top:]), sizes
+    assert sizes[top] > 0 and max(sizes) == sizes[top]
+    enc.free()
+
+
+def test_encoder_calls_from_two_threads_on_two_streams(dev, orc):
+    """Two host threads, each on its own stream, call one encoder four times each with different lengths: the calls
+    are serialized and ordered on the device, so every output equals the one-at-a-time result."""
+    import threading
+
+    import torch
+
+    enc, params = _small_encoder()
+    jobs = {0: [(29, 1), (64, 2), (29, 3), (101, 4)], 1: [(64, 5), (29, 6), (77, 7), (64, 8)]}
+    inputs = {seed: _x(400 + seed, t, 256) for lst in jobs.values() for t, seed in lst}
+    want = {seed: _oracle_stack(orc, inputs[seed], params, 2) for seed in inputs}
+    got, errors = {}, []
+
+    def worker(k):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for t, seed in jobs[k]:
+                    got[seed] = enc.forward(_t(inputs[seed], dev))
+            s.synchronize()
+        except Exception as e:  # reported by the main thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in jobs]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for seed, w in want.items():
+        _bits_equal(got[seed].cpu().numpy(), w, f"threaded call {seed}")
+    enc.free()
+
+
+def test_encoder_profile_sums_sublayers(dev, orc):
+    """With profiling on (the reference's VOXRT_PROFILE), a forward reports device time per sublayer type; the types
+    add up to the total and the output is the same as without profiling."""
+    enc, params = _small_encoder()
+    x = _x(500, 88, 256)
+    want = _oracle_stack(orc, x, params, 2)
+    enc.set_profiling(True)
+    got = enc.forward(_t(x, dev)).cpu().numpy()
+    p = enc.take_profile()
+    _bits_equal(got, want, "profiled forward")
+    assert p["forwards"] == 1
+    parts = [p[k] for k in ("subsampling_ms", "ff_ms", "attn_ms", "conv_ms", "norm_ms")]
+    assert all(v > 0 for v in parts[1:]) and p["attn_core_ms"] > 0
+    assert abs(sum(parts) - p["total_ms"]) <= 0.02 * p["total_ms"] + 1e-3
+    assert enc.take_profile()["forwards"] == 0
+    enc.set_profiling(False)
+    _bits_equal(enc.forward(_t(x, dev)).cpu().numpy(), want, "after profiling")
+    enc.free()

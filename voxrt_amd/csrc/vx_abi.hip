@@ -50,6 +50,9 @@ void encoder_use_graphs(vx_encoder *e, bool on);
 void encoder_set_layer(vx_encoder *e, int64_t li, const vx_layer_params *p);
 void encoder_set_subsampling(vx_encoder *e, const vx_subsampling_params *p);
 void encoder_forward(vx_encoder *e, const float *x, float *out, int64_t t, hipStream_t st);
+void encoder_set_profiling(vx_encoder *e, bool on);
+void encoder_take_profile(vx_encoder *e, vx_encoder_profile *out);
+void encoder_memory(vx_encoder *e, int64_t *workspace_bytes, int64_t *graphs);
 void encoder_forward_batch(vx_encoder *e, const float *x, float *out, int64_t nseg, int64_t t, hipStream_t st);
 void encoder_forward_feats_batch(vx_encoder *e, const float *feats, int64_t nseg, int64_t t_in, float *out,
                                  int64_t *t_out, hipStream_t st);
@@ -321,6 +324,18 @@ vx_status vx_encoder_set_subsampling(vx_encoder *enc, const vx_subsampling_param
 
 vx_status vx_encoder_use_graphs(vx_encoder *enc, int on) {
     return guarded([&] { vx::encoder_use_graphs(enc, on != 0); });
+}
+
+vx_status vx_encoder_set_profiling(vx_encoder *enc, int on) {
+    return guarded([&] { vx::encoder_set_profiling(enc, on != 0); });
+}
+
+vx_status vx_encoder_take_profile(vx_encoder *enc, vx_encoder_profile *out) {
+    return guarded([&] { vx::encoder_take_profile(enc, out); });
+}
+
+vx_status vx_encoder_memory(vx_encoder *enc, int64_t *workspace_bytes, int64_t *graphs) {
+    return guarded([&] { vx::encoder_memory(enc, workspace_bytes, graphs); });
 }
 
 vx_status vx_encoder_forward(vx_encoder *enc, const float *x, float *out, int64_t t, void *stream) {

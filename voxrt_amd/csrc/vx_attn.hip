@@ -432,6 +432,23 @@ size_t attn_ws_bytes_seg(int64_t t, int64_t d, int64_t h, int64_t nseg) {
 
 size_t attn_ws_bytes(int64_t t, int64_t d, int64_t h) { return attn_ws_bytes_seg(t, d, h, 1); }
 
+// The dynamic-LDS limit of the core kernels (above the 64 KiB default), raised once per device; thread-safe, devices
+// past 63 every call. Callers that capture launches into a graph call it before the capture.
+void attention_prime() {
+    static std::atomic<bool> lds_raised[64];
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    const bool cached = dev >= 0 && dev < 64;
+    if (cached && lds_raised[dev].load(std::memory_order_acquire)) return;
+    hip_check(hipFuncSetAttribute((const void *)attn_core_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024),
+              "attention LDS limit");
+    hip_check(hipFuncSetAttribute((const void *)attn_core_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024),
+              "attention LDS limit");
+    if (cached) lds_raised[dev].store(true, std::memory_order_release);
+}
+
 // ctx [nseg][t][d] from qkv [nseg][t][3d] (q | k | v) and the shared rel_k [2t-1][d] of t frames: each segment's
 // attention on its own tokens; ws is attn_ws_bytes_seg(t, d, h, nseg) device bytes.
 // With q (and scales_t, gsum_t) not NULL, ctx is not written: the o-projection's activations are, in 128-column
@@ -473,20 +490,7 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
                                                                          rows_blocks);
     hip_check(hipGetLastError(), "attention rows / vT kernel launch");
     const size_t lds = core_lds_bytes((int)t);
-    // the dynamic-LDS limit of the core kernels, raised once per device (thread-safe; devices past 63 every call)
-    static std::atomic<bool> lds_raised[64];
-    int dev = 0;
-    hip_check(hipGetDevice(&dev), "hipGetDevice");
-    const bool cached = dev >= 0 && dev < 64;
-    if (!cached || !lds_raised[dev].load(std::memory_order_acquire)) {
-        hip_check(hipFuncSetAttribute((const void *)attn_core_kernel<false>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
-                  "attention LDS limit");
-        hip_check(hipFuncSetAttribute((const void *)attn_core_kernel<true>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
-                  "attention LDS limit");
-        if (cached) lds_raised[dev].store(true, std::memory_order_release);
-    }
+    attention_prime();
     AttnQOut Q{q, scales_t, gsum_t, (int)((nseg * t + 15) / 16 * 16)};
     const dim3 grid((unsigned)(D.tp / 16), (unsigned)h, (unsigned)nseg);
     if (qout)

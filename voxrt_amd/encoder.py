@@ -10,7 +10,9 @@
   rel_pos_table          encoder.rs:760-776
   attention_core         encoder.rs:317-534 (attn_core_int8, all heads)
   Encoder                GpuEncoder::{load, forward, forward_feats} (metal/mod.rs:446-603) with the CPU int8
-                         Encoder's operation order (encoder.rs:706-857); one hipGraph per frame count
+                         Encoder's operation order (encoder.rs:706-857); one grow-only workspace, a bounded cache
+                         of hipGraphs by (frames, segments); VOXRT_PROFILE=1 prints the per-sublayer profile of
+                         every forward to stderr (encoder.rs:823-854)
 
 Device tensors are torch tensors on the current HIP device; calls are ordered on torch's current stream. Nothing
 here has a CPU fallback: every op is a HIP kernel of the library.
@@ -18,6 +20,8 @@ here has a CPU fallback: every op is a HIP kernel of the library.
 from __future__ import annotations
 
 import ctypes as C
+import os
+import sys
 
 import numpy as np
 
@@ -267,6 +271,11 @@ class _SubParams(C.Structure):
     _fields_ = [(k, C.c_void_p) for k in SUB_KEYS]
 
 
+class _Profile(C.Structure):
+    _fields_ = [(n, C.c_double) for n in ("total_ms", "subsampling_ms", "ff_ms", "attn_ms", "attn_core_ms", "conv_ms",
+                                          "norm_ms")] + [("forwards", C.c_int64)]
+
+
 class Encoder:
     """The FastConformer encoder on one GPU, int8 path (vx_encoder_*)."""
 
@@ -278,6 +287,9 @@ class Encoder:
         self._h = h
         self.d, self.heads, self.ff, self.kconv, self.group, self.n_layers = d, heads, ff, kconv, group, n_layers
         self.n_mels, self.sub_channels, self.sub_kernel, self.sub_stride = n_mels, sub_channels, sub_kernel, sub_stride
+        self._print_profile = os.environ.get("VOXRT_PROFILE") is not None
+        if self._print_profile:
+            self.set_profiling(True)
 
     def set_layer(self, i: int, p: dict) -> None:
         """p: {"linears": {name: (qweight, scales_f16)}, "norms": {name: (g, b)}, "bias_u", "bias_v", "dw" [d, k],
@@ -332,6 +344,30 @@ class Encoder:
     def use_graphs(self, on: bool) -> None:
         check(lib().vx_encoder_use_graphs(self._h, int(on)))
 
+    def set_profiling(self, on: bool) -> None:
+        """Per-sublayer device timing of every forward (kernels launched one by one, events between sublayers)."""
+        check(lib().vx_encoder_set_profiling(self._h, int(on)))
+
+    def take_profile(self) -> dict:
+        """Milliseconds per sublayer type summed over layers and over the forwards since the last take."""
+        p = _Profile()
+        check(lib().vx_encoder_take_profile(self._h, C.byref(p)))
+        return {n: getattr(p, n) for n, _ in _Profile._fields_}
+
+    def memory(self) -> tuple:
+        """(workspace device bytes, graphs kept)."""
+        b, g = C.c_int64(), C.c_int64()
+        check(lib().vx_encoder_memory(self._h, C.byref(b), C.byref(g)))
+        return int(b.value), int(g.value)
+
+    def _after_forward(self, t: int) -> None:
+        if self._print_profile:  # the reference's eprintln! line (encoder.rs:845-854), device times
+            p = self.take_profile()
+            print(f"encoder profile (Int8, HIP, T_e={t}): total {p['total_ms'] / 1e3:.3f}s · subsampling "
+                  f"{p['subsampling_ms'] / 1e3:.3f} · ff {p['ff_ms'] / 1e3:.3f} · attn {p['attn_ms'] / 1e3:.3f} (core "
+                  f"{p['attn_core_ms'] / 1e3:.3f}) · conv {p['conv_ms'] / 1e3:.3f} · norm {p['norm_ms'] / 1e3:.3f}",
+                  file=sys.stderr)
+
     def forward(self, x, out=None):
         """The layer stack on x [t, d] (the subsampling output); returns out [t, d]."""
         import torch
@@ -340,6 +376,7 @@ class Encoder:
         out = torch.empty_like(x) if out is None else out
         check(lib().vx_encoder_forward(self._h, _f32(x, "x", (t, self.d)), _f32(out, "out", (t, self.d)), t,
                                        K._stream()))
+        self._after_forward(t)
         return out
 
     def out_frames(self, t_in: int) -> int:
@@ -355,6 +392,7 @@ class Encoder:
         got = C.c_int64()
         check(lib().vx_encoder_forward_feats(self._h, _f32(feats, "feats", (t_in, self.n_mels)), t_in,
                                              _f32(out, "out", (t3, self.d)), C.byref(got), K._stream()))
+        self._after_forward(t3)
         return out
 
     def forward_batch(self, x, out=None):
@@ -366,6 +404,7 @@ class Encoder:
         out = torch.empty_like(x) if out is None else out
         check(lib().vx_encoder_forward_batch(self._h, _f32(x, "x", (nseg, t, self.d)),
                                              _f32(out, "out", (nseg, t, self.d)), nseg, t, K._stream()))
+        self._after_forward(t)
         return out
 
     def forward_feats_batch(self, feats, out=None):
@@ -380,6 +419,7 @@ class Encoder:
         check(lib().vx_encoder_forward_feats_batch(self._h, _f32(feats, "feats", (nseg, t_in, self.n_mels)), nseg,
                                                    t_in, _f32(out, "out", (nseg, t3, self.d)), C.byref(got),
                                                    K._stream()))
+        self._after_forward(t3)
         return out
 
     def free(self) -> None:

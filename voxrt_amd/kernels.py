@@ -87,6 +87,9 @@ def lib() -> C.CDLL:
             "vx_encoder_forward_batch": (I, [P, P, P, I64, I64, P]),
             "vx_encoder_forward_feats_batch": (I, [P, P, I64, I64, P, C.POINTER(I64), P]),
             "vx_encoder_free": (None, [P]),
+            "vx_encoder_set_profiling": (I, [P, I]),
+            "vx_encoder_take_profile": (I, [P, P]),
+            "vx_encoder_memory": (I, [P, C.POINTER(I64), C.POINTER(I64)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
