@@ -598,7 +598,7 @@ def test_wrappers_refuse_tensors_of_the_wrong_shape(dev):
         vx.gemm_rows_range(w, x, y[:4], 0, out, 0, 4)
     with pytest.raises(ValueError, match="bias"):
         vx.gemm_single(w, x, y, short)
-    bad = vx.QuantAct(x.x, x.scales_t[:, :8], x.gsum_t, n, inp, 128)
+    bad = vx.QuantAct(x.x, x.scales_t[:, :8].contiguous(), x.gsum_t, n, inp, 128)
     with pytest.raises(ValueError, match="scales_t"):
         vx.gemm_ep(w, bad, y)
     with pytest.raises(ValueError, match="gamma"):
