@@ -197,6 +197,16 @@ vx_status vx_attention_core(const float *qkv, const float *rel_k, int64_t t, int
                             const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
                             void *stream);
 
+/* NO COUNTERPART IN THE REFERENCE. vx_attention_core without the ws argument, for callers that cannot allocate
+ * device memory (code under graph capture, serving loops or harnesses that forbid hipMalloc): the workspace is a
+ * fixed 8 MiB array in the library, one per GPU, held until the process ends (its address is looked up by vx_init,
+ * or by the first call on a device). Calls whose vx_attention_ws_bytes(t, d, h) exceeds 8 MiB are refused with
+ * VX_ERR_INVALID (t <= 1024 with d = 1024 and 8 heads fits). Nothing is allocated. All calls on one GPU share the
+ * array: calls that overlap on one GPU (other streams, other threads) race; serialize them. */
+vx_status vx_attention_core_noalloc(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h,
+                                    const float *bias_u, const float *bias_v, float scaling, float *ctx,
+                                    void *stream);
+
 /* attention core + prepare fused (Attention::forward_fused, encoder.rs:180-183: attn_core_int8 into ctx, then
  * wo.prepare(ctx)): as vx_attention_core, but ctx is written as the o-projection's int8 activations in 128-column
  * groups, one per head (group must be 128): q int8 [t, d], scales_t float32 and gsum_t int32 [h, VX_NPAD(t)]

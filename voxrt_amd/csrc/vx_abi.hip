@@ -41,6 +41,9 @@ void check_activations(uint64_t *mismatch_host);
 size_t attn_ws_bytes(int64_t t, int64_t d, int64_t h);
 void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h, const float *bias_u,
                     const float *bias_v, float scaling, void *ws, float *ctx, hipStream_t st);
+void attention_core_noalloc(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h,
+                            const float *bias_u, const float *bias_v, float scaling, float *ctx, hipStream_t st);
+void *static_attn_ws();
 void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
                         const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
                         hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t, int64_t rel_ld);
@@ -117,6 +120,7 @@ vx_status vx_init(int device) {
         if (device < 0 || device >= n) throw vx::Error(VX_ERR_INVALID, "device index out of range");
         if (!is_gfx950(device)) throw vx::Error(VX_ERR_NO_DEVICE, "device is not gfx950 (MI355X)");
         vx::hip_check(hipSetDevice(device), "hipSetDevice");
+        (void)vx::static_attn_ws();  // the device address of the workspace-free attention core's array
     });
 }
 
@@ -292,6 +296,13 @@ vx_status vx_attention_core(const float *qkv, const float *rel_k, int64_t t, int
                             void *stream) {
     return guarded([&] {
         vx::attention_core(qkv, rel_k, t, d, h, bias_u, bias_v, scaling, ws, ctx, (hipStream_t)stream);
+    });
+}
+
+vx_status vx_attention_core_noalloc(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h,
+                                    const float *bias_u, const float *bias_v, float scaling, float *ctx, void *stream) {
+    return guarded([&] {
+        vx::attention_core_noalloc(qkv, rel_k, t, d, h, bias_u, bias_v, scaling, ctx, (hipStream_t)stream);
     });
 }
 

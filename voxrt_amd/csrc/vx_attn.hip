@@ -20,6 +20,7 @@
 //                       running sums per row on four lanes, so the order is the reference's); the probabilities
 //                       quantized into LDS; P . vT through the same MFMA; ctx written in place in [t][d].
 #include <atomic>
+#include <string>
 
 #include "vx_internal.h"
 
@@ -498,6 +499,49 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
     else
         attn_core_kernel<false><<<grid, 256, lds, st>>>(D, W, scaling, ctx, Q);
     hip_check(hipGetLastError(), "attention core kernel launch");
+}
+
+// ---------------------------------------------------------------- the attention core without a caller workspace
+//
+// For callers that cannot allocate device memory (code under graph capture, serving loops that forbid it): the
+// workspace is this file-scope array, one copy per GPU, held until the process ends. Its size bounds the calls:
+// attn_ws_bytes(t, d, h) <= kStaticAttnWsBytes (t <= 1024 frames with d = 1024, 8 heads, needs 6.4 MiB). All calls
+// on one GPU share its array, which keeps the previous call's contents: the preparation kernel writes every byte
+// the core kernel then reads, so nothing needs clearing, and calls that overlap on one GPU race.
+constexpr size_t kStaticAttnWsBytes = 8u << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticAttnWsBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void *> scratch_addr[kMaxDevices];
+}  // namespace
+
+// The device address of `scratch` on the current device (the host-side name is only a stand-in): looked up once per
+// device with hipGetSymbolAddress and kept.
+void *static_attn_ws() {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    require(dev >= 0 && dev < kMaxDevices, "attention without a workspace: device index above 63");
+    void *p = scratch_addr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(attention scratch)");
+        require(p != nullptr, "hipGetSymbolAddress(attention scratch) returned NULL");
+        scratch_addr[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
+void attention_core_noalloc(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h,
+                            const float *bias_u, const float *bias_v, float scaling, float *ctx, hipStream_t st) {
+    require(h > 0 && d == h * kDh, "attention: the head dimension must be 128");
+    require(t >= 1 && t <= 1024, "attention: 1 <= t <= 1024 frames");
+    const size_t need = attn_ws_bytes(t, d, h);
+    require(need <= kStaticAttnWsBytes, "attention without a workspace: t = " + std::to_string(t) + ", " +
+                                            std::to_string(h) + " heads need " + std::to_string(need) +
+                                            " bytes of workspace, above the fixed " +
+                                            std::to_string(kStaticAttnWsBytes) + " (use vx_attention_core)");
+    attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, static_attn_ws(), ctx, st, nullptr, nullptr,
+                       nullptr, d);
 }
 
 // ctx [t][d] from qkv [t][3d] (q | k | v) and rel_k [2t-1][d]; ws is attn_ws_bytes(t, d, h) device bytes.

@@ -77,6 +77,7 @@ def lib() -> C.CDLL:
             "vx_attention_ws_bytes": (I64, [I64, I64, I64]),
             "vx_check_activations": (I, [P]),
             "vx_attention_core": (I, [P, P, I64, I64, I64, P, P, F, P, P, P]),
+            "vx_attention_core_noalloc": (I, [P, P, I64, I64, I64, P, P, F, P, P]),
             "vx_attention_core_quantize": (I, [P, P, I64, I64, I64, P, P, F, P, I64, P, P, P, P]),
             "vx_encoder_create": (I, [P, C.POINTER(P)]),
             "vx_encoder_set_layer": (I, [P, I64, P]),
