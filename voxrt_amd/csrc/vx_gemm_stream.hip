@@ -1,8 +1,8 @@
 // vx_gemm_stream.hip — persistent large-token ternary x int8 GEMM (one group, G = K) on gfx950 i8 MFMA, bit-exact
 // to voxrt's scalar kernel (crates/voxrt/src/kernels/mod.rs:166-210): y[t, o] = ep(fma((float)S, xs[t] * ws[o], 0)).
 //
-// One workgroup of 4 wavefronts per CU walks a sequence of 128-token x 256-row output tiles; wavefront w owns the
-// tile's rows [64w, 64w + 64). The tiles of XCD x (workgroup b runs on XCD b % 8) are a contiguous range of the
+// One workgroup of 4 wavefronts per CU (two per CU for the SiLU epilogue with K = 1024, each with half the LDS ring)
+// walks a sequence of 128-token x 256-row output tiles; wavefront w owns the tile's rows [64w, 64w + 64). The tiles of XCD x (workgroup b runs on XCD b % 8) are a contiguous range of the
 // row-major tile order, so the workgroups of one XCD work on the same token rows at the same time and its L2 cache
 // serves their activation tiles and the weight plane.
 //
@@ -43,22 +43,30 @@
 namespace vx {
 namespace {
 
+// Two workgroups per CU (two wavefronts per SIMD) for the SiLU epilogue with K = 1024: its epilogue's VALU work
+// (about 24 instructions per output) then overlaps the other workgroup's MFMAs. Measured at 8192 tokens: FFN-up
+// SiLU 62.7-64.5 -> 53.4-56.7 us; the Store epilogue (40 -> 46 us) and K = 4096 (35 -> 42 us) are slower so.
+constexpr bool occ2_of(int ep, bool k16) { return ep == VX_EP_SILU && k16; }
+
 // Loads run kPD steps ahead of use. When step s begins, the loads of step s+1 (the first instructions of step
 // s+1-kPD) must be complete: the vector-memory instructions issued after them are 2 stores of that step and 5 per
 // later step (3 DMA + 2 stores), plus the 4 scale DMAs issued after the loads of tile step nk-kPD.
-constexpr int kPD = 6;
 constexpr int kEarly = 2;  // token rows of MFMAs issued before a step's loads (the matrix pipe stays busy)
 constexpr int kValuPerDs = 2;    // VALU instructions placed beside each fragment read (with its MFMA)
 constexpr int kValuPerMfma = 3;  // VALU instructions after each remaining MFMA (one MFMA is 16 cycles)
-__device__ constexpr int wait_of(int i, int nk) { return 2 + 5 * (kPD - 2) + ((i >= nk - kPD + 1) ? 4 : 0); }
+__device__ constexpr int wait_of(int pd, int i, int nk) { return 2 + 5 * (pd - 2) + ((i >= nk - pd + 1) ? 4 : 0); }
 
-template <int EP, bool BIAS, bool K16>
-__global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, const StreamGeom g) {
+template <int EP, bool BIAS, bool K16, bool OCC2>
+__global__ __launch_bounds__(256, OCC2 ? 2 : 1) void tgemm_stream_kernel(const GemmArgs a, const StreamGeom g) {
+    // OCC2: two workgroups per CU (two wavefronts per SIMD), each with half the LDS ring and one accumulator set, so
+    // that one workgroup's epilogue, waits and barriers overlap the other's MFMAs
+    constexpr int kPD = OCC2 ? 3 : 6;  // steps the loads run ahead
+    constexpr int NS = OCC2 ? 4 : 8;   // LDS slots
     // DRAIN: every tile's epilogue after its last step, one accumulator set. Measured at 8192 tokens: faster for
     // SiLU (its VALU work made the steps of the next tile VALU-bound: 67 -> 62 us for FFN-up) and for K > 1024
     // (FFN-down 32.7 -> 31.4 us); the Store epilogue with K = 1024 keeps the two-blocks-per-step overlap
     // (40 us against 43).
-    constexpr bool DRAIN = EP != VX_EP_STORE || !K16;
+    constexpr bool DRAIN = OCC2 || EP != VX_EP_STORE || !K16;
     typedef __attribute__((address_space(3))) void lds_void;
     // one LDS object per activation slot and per scale table: the compiler then sees that a DMA into one slot
     // does not alias the fragment reads of another and adds no vmcnt wait of its own before them
@@ -71,9 +79,11 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
     __shared__ __attribute__((aligned(16))) float xs0[256], xs1[256], gs0[256], gs1[256], ws0[256], ws1[256],
         bi0[256], bi1[256];
     auto sact = [&](int i) -> int8_t * {
+        if constexpr (NS == 4) return i == 0 ? sa0 : i == 1 ? sa1 : i == 2 ? sa2 : sa3;
         return i == 0 ? sa0 : i == 1 ? sa1 : i == 2 ? sa2 : i == 3 ? sa3 : i == 4 ? sa4 : i == 5 ? sa5 : i == 6 ? sa6 : sa7;
     };
     auto swt = [&](int i) -> uint32_t * {
+        if constexpr (NS == 4) return i == 0 ? sw0 : i == 1 ? sw1 : i == 2 ? sw2 : sw3;
         return i == 0 ? sw0 : i == 1 ? sw1 : i == 2 ? sw2 : i == 3 ? sw3 : i == 4 ? sw4 : i == 5 ? sw5 : i == 6 ? sw6 : sw7;
     };
     auto ssc = [&](int par, int kind) -> float * {
@@ -159,11 +169,13 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wsrs, (lds_void *)ssc(par, 2), 16, vo, 0, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (lds_void *)ssc(par, 3), 16, BIAS ? vo : kOff, 0, 0, 0);
     };
-    v4i fr[2][8];
+    constexpr int NFS = OCC2 ? 1 : 2;  // fragment sets: OCC2 reads the next step's fragment of a token block
+                                       // into the registers its last MFMA of this step has just read
+    v4i fr[NFS][8];
     uint32_t rw[4];
     auto read_frags = [&](int slot, int set) {
 #pragma unroll
-        for (int tb = 0; tb < 8; tb++) fr[set][tb] = *(const v4i *)(sact(slot) + tb * 1024 + vfr);
+        for (int tb = 0; tb < 8; tb++) fr[set % NFS][tb] = *(const v4i *)(sact(slot) + tb * 1024 + vfr);
     };
     auto read_weights = [&](int slot) {
 #pragma unroll
@@ -191,6 +203,14 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
         c.bia = make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (BIAS) c.bia = *(const float4 *)&ssc(par, 3)[wave * 64 + ob * 16 + lq * 4];
         return c;
+    };
+    // Two stores that write nothing (offsets past the buffer end) where a step has no output blocks to store, so
+    // that every step issues the same vector-memory instructions. Their offsets differ: two identical stores would
+    // be merged into one by the compiler, and the wait counts, which assume two, would no longer cover the loads.
+    auto dummy_stores = [&]() {
+        const v4i z{0, 0, 0, 0};
+        __builtin_amdgcn_raw_buffer_store_b128(z, yrs, kOff, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(z, yrs, kOff - 16, 0, 0);
     };
     auto out_block = [&](const v4i (&acc)[8][4], const BlockScales &c, int tb, int ob, uint32_t vy, uint32_t sy) {
         const float xs = c.xs;
@@ -237,15 +257,15 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
             sc0 = block_scales(PAR ^ 1, CH / 2, 2 * (CH % 2));
             sc1 = block_scales(PAR ^ 1, CH / 2, 2 * (CH % 2) + 1);
         }
-        read_weights((SLOT + 1) & 7);
+        read_weights((SLOT + 1) % NS);
         constexpr int fs = SLOT & 1;
         auto mfma_row = [&](int tb) {
 #pragma unroll
             for (int ob = 0; ob < 4; ob++) {
                 if constexpr (CH == 0)  // tile step 0: the chains start from zero
-                    acc[tb][ob] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[fs][ob], fr[fs][tb], v4i{0, 0, 0, 0}, 0, 0, 0);
+                    acc[tb][ob] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[fs][ob], fr[fs % NFS][tb], v4i{0, 0, 0, 0}, 0, 0, 0);
                 else
-                    acc[tb][ob] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[fs][ob], fr[fs][tb], acc[tb][ob], 0, 0, 0);
+                    acc[tb][ob] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[fs][ob], fr[fs % NFS][tb], acc[tb][ob], 0, 0, 0);
             }
         };
         // the first kEarly token rows of MFMAs go before this step's loads, so that the matrix pipe is busy while
@@ -253,20 +273,18 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
         static_for<0, kEarly>([&](auto T) { mfma_row(decltype(T)::value); });
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (NEXT)
-            dma((SLOT + kPD) & 7, i + kPD - nk, vdma_nxt, sa_nxt, vw_nxt, sw_nxt);
+            dma((SLOT + kPD) % NS, i + kPD - nk, vdma_nxt, sa_nxt, vw_nxt, sw_nxt);
         else
-            dma((SLOT + kPD) & 7, i + kPD, vdma, sa_cur, vwd, sw_cur);
+            dma((SLOT + kPD) % NS, i + kPD, vdma, sa_cur, vwd, sw_cur);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (SCALE) scale_dma(PAR, true);
-        read_frags((SLOT + 1) & 7, (SLOT + 1) & 1);
+        read_frags((SLOT + 1) % NS, (SLOT + 1) & 1);
         static_for<kEarly, 8>([&](auto T) { mfma_row(decltype(T)::value); });
         if constexpr (CHUNK) {
             out_block(accp, sc0, CH / 2, 2 * (CH % 2), vy_p, sy_p);
             out_block(accp, sc1, CH / 2, 2 * (CH % 2) + 1, vy_p, sy_p);
         } else {
-            const v4i z{0, 0, 0, 0};
-            __builtin_amdgcn_raw_buffer_store_b128(z, yrs, kOff, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(z, yrs, kOff, 0, 0);
+            dummy_stores();
         }
         widen(fs ^ 1);
         // issue order: the 8 fragment reads of the next step each after an MFMA with 2 VALU, then 3 VALU after
@@ -285,6 +303,49 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
         __builtin_amdgcn_sched_barrier(0);
     };
 
+    // OCC2 step: the same loads, one fragment set. After the four MFMAs of token block tb, the next step's fragment
+    // of tb is read into the same registers; the next step's weights are widened beside the MFMAs.
+    auto step2 = [&](auto Wc, auto SLOTc, auto CHc, auto NEXTc, auto SCALEc, auto PARc, int i, v4i(&acc)[8][4]) {
+        constexpr int W = decltype(Wc)::value, SLOT = decltype(SLOTc)::value, CH = decltype(CHc)::value;
+        constexpr bool NEXT = decltype(NEXTc)::value != 0, SCALE = decltype(SCALEc)::value != 0;
+        constexpr int PAR = decltype(PARc)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(W));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        read_weights((SLOT + 1) % NS);
+        constexpr int fs = SLOT & 1;
+        constexpr int nslot = (SLOT + 1) % NS;
+        auto mfma_row = [&](int tb) {
+#pragma unroll
+            for (int ob = 0; ob < 4; ob++) {
+                if constexpr (CH == 0)
+                    acc[tb][ob] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[fs][ob], fr[0][tb], v4i{0, 0, 0, 0}, 0, 0, 0);
+                else
+                    acc[tb][ob] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[fs][ob], fr[0][tb], acc[tb][ob], 0, 0, 0);
+            }
+            fr[0][tb] = *(const v4i *)(sact(nslot) + tb * 1024 + vfr);
+        };
+        static_for<0, kEarly>([&](auto T) { mfma_row(decltype(T)::value); });
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NEXT)
+            dma((SLOT + kPD) % NS, i + kPD - nk, vdma_nxt, sa_nxt, vw_nxt, sw_nxt);
+        else
+            dma((SLOT + kPD) % NS, i + kPD, vdma, sa_cur, vwd, sw_cur);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (SCALE) scale_dma(PAR, true);
+        dummy_stores();
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<kEarly, 8>([&](auto T) { mfma_row(decltype(T)::value); });
+        widen(fs ^ 1);
+#pragma unroll
+        for (int k = 0; k < 4 * (8 - kEarly); k++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
     // whole epilogue of a tile at once (after its last step): AddScaled tiles, and the last tile of the sequence
     auto drain = [&](auto PARc, const v4i(&acc)[8][4]) {
         constexpr int PAR = decltype(PARc)::value;
@@ -295,7 +356,18 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
 #pragma unroll
         for (int tb = 0; tb < 8; tb++)
 #pragma unroll
-            for (int ob = 0; ob < 4; ob++) out_block(acc, block_scales(PAR, tb, ob), tb, ob, vyl, sy);
+            for (int ob = 0; ob < 4; ob++) {
+                out_block(acc, block_scales(PAR, tb, ob), tb, ob, vyl, sy);
+                if constexpr (OCC2) __builtin_amdgcn_sched_barrier(0);  // one block's registers at a time
+            }
+    };
+
+    auto stepx = [&](auto Wc, auto SLOTc, auto CHc, auto NEXTc, auto SCALEc, auto PARc, int i, v4i(&acc)[8][4],
+                     const v4i(&accp)[8][4]) {
+        if constexpr (OCC2)
+            step2(Wc, SLOTc, CHc, NEXTc, SCALEc, PARc, i, acc);
+        else
+            step(Wc, SLOTc, CHc, NEXTc, SCALEc, PARc, i, acc, accp);
     };
 
     // one tile: steps 0..nk-1 into `acc` (tile parity PAR), the pending tile's epilogue from `accp`
@@ -305,25 +377,26 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
         if constexpr (K16) {
             static_for<0, 16>([&](auto I) {
                 constexpr int i = decltype(I)::value;
-                step(IC<wait_of(i, 16)>{}, IC<i % 8>{}, IC<i>{}, IC<(i >= 16 - kPD)>{}, IC<i == 16 - kPD>{}, IC<PAR>{},
-                     i, acc, accp);
+                stepx(IC<wait_of(kPD, i, 16)>{}, IC<i % NS>{}, IC<i>{}, IC<(i >= 16 - kPD)>{}, IC<i == 16 - kPD>{},
+                      IC<PAR>{}, i, acc, accp);
             });
         } else {
             static_for<0, 16>([&](auto I) {
                 constexpr int i = decltype(I)::value;
-                step(IC<wait_of(0, 64)>{}, IC<i % 8>{}, IC<i>{}, IC<0>{}, IC<0>{}, IC<PAR>{}, i, acc, accp);
+                stepx(IC<wait_of(kPD, 0, 64)>{}, IC<i % NS>{}, IC<i>{}, IC<0>{}, IC<0>{}, IC<PAR>{}, i, acc, accp);
             });
             // steps 16 .. nk-9 in groups of 8 (slot positions stay compile-time: nk % 8 == 0)
             for (int i0 = 16; i0 < nk - 8; i0 += 8) {
                 static_for<0, 8>([&](auto P) {
                     constexpr int p = decltype(P)::value;
-                    step(IC<wait_of(0, 64)>{}, IC<p>{}, IC<-1>{}, IC<0>{}, IC<0>{}, IC<PAR>{}, i0 + p, acc, accp);
+                    stepx(IC<wait_of(kPD, 0, 64)>{}, IC<p % NS>{}, IC<-1>{}, IC<0>{}, IC<0>{}, IC<PAR>{}, i0 + p, acc,
+                          accp);
                 });
             }
             static_for<0, 8>([&](auto P) {
                 constexpr int p = decltype(P)::value;
-                step(IC<wait_of(56 + p, 64)>{}, IC<p>{}, IC<-1>{}, IC<(p >= 8 - kPD)>{}, IC<p == 8 - kPD>{}, IC<PAR>{},
-                     nk - 8 + p, acc, accp);
+                stepx(IC<wait_of(kPD, 56 + p, 64)>{}, IC<p % NS>{}, IC<-1>{}, IC<(p >= 8 - kPD)>{}, IC<p == 8 - kPD>{},
+                      IC<PAR>{}, nk - 8 + p, acc, accp);
             });
         }
         // this tile becomes the pending one (or is written now: AddScaled, or the last tile)
@@ -345,14 +418,12 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
     // prologue: the instruction pattern of tile steps nk-4 .. nk-1 of a virtual previous tile (dummy scale DMAs
     // and stores), loading steps 0..3 of the first tile
     {
-        const v4i z{0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < kPD; i++) {
             dma(i, i, vdma, sa_cur, vwd, sw_cur);
             __builtin_amdgcn_sched_barrier(0);
             if (i == 0) scale_dma(1, false);
-            __builtin_amdgcn_raw_buffer_store_b128(z, yrs, kOff, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(z, yrs, kOff, 0, 0);
+            dummy_stores();
             __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 + 2 + 5 * (kPD - 1)));  // the loads of step 0 complete
@@ -379,9 +450,9 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_kernel(const GemmArgs a, 
 template <int EP, bool BIAS>
 void launch_stream(const GemmArgs &a, const StreamGeom &g, int grid, hipStream_t st) {
     if (g.nk == 16)
-        tgemm_stream_kernel<EP, BIAS, true><<<grid, 256, 0, st>>>(a, g);
+        tgemm_stream_kernel<EP, BIAS, true, occ2_of(EP, true)><<<grid, 256, 0, st>>>(a, g);
     else
-        tgemm_stream_kernel<EP, BIAS, false><<<grid, 256, 0, st>>>(a, g);
+        tgemm_stream_kernel<EP, BIAS, false, occ2_of(EP, false)><<<grid, 256, 0, st>>>(a, g);
 }
 
 }  // namespace
@@ -417,7 +488,7 @@ bool gemm_stream(const GemmArgs &a, int tokens_full, hipStream_t st) {
     g.ng = 1;
     const int cus = cu_count();
     if (g.ntiles < cus && !(kv && *kv)) return false;  // too few tiles to fill the chip: the other kernels
-    int per_x = std::min(cus / 8, g.per_xcd);
+    int per_x = std::min((occ2_of(a.ep, nk == 16) ? 2 : 1) * cus / 8, g.per_xcd);
     const char *ge = getenv("VX_STREAM_GRID");  // workgroups (a multiple of 8): tuning and tests
     if (ge && *ge && atoi(ge) >= 8) per_x = std::min(atoi(ge) / 8, g.per_xcd);
     const int grid = 8 * per_x;
