@@ -29,6 +29,8 @@
  *   vx_encoder_memory                 <- (none: the workspace size and graph count, for hosts that bound memory)
  *   vx_last_error                     <- voxrt_last_error (crates/voxrt-ffi/src/lib.rs:61-74)
  *   vx_check_activations              <- (none: device self-check of exp_poly/silu_fast/sigmoid_fast)
+ *   vx_set_kernel_override            <- VOXRT_KERNEL's role for the GPU kernels (kernels/mod.rs:126-149): forcing
+ *                                        a kernel family, tile or grid for tests and tuning
  *
  * Conventions (as voxrt-ffi): every call returns a vx_status; on failure a message is kept in a thread-local
  * buffer read by vx_last_error(). No exception crosses the ABI. Weight uploads take HOST pointers (the load-time
@@ -73,6 +75,13 @@ int vx_detect(void);
 
 /* Make `device` current for this thread and check that it is gfx950. */
 vx_status vx_init(int device);
+
+/* Force a GEMM kernel choice for the whole process (tests and tuning; the library reads no environment variable):
+ * name "gemm" with value direct | splitk | lds | big | splitg | small | stream, "tile" and "small_tile" with "MTxNT"
+ * (16*MT tokens x 16*NT rows), "stream_grid" with a workgroup count (a multiple of 8). A forced kernel that cannot
+ * run a shape is not used for it. NULL or "" clears the override of that name. Not for concurrent use with GEMM
+ * calls that should not see it. */
+vx_status vx_set_kernel_override(const char *name, const char *value);
 
 /* Wait for all work on the current device and report any error it left. No counterpart in voxrt (its GPU
  * context lives until the process drops it); for hosts that end a device session explicitly. The library keeps no

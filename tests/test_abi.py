@@ -109,3 +109,22 @@ def test_encoder_parameters_are_checked_on_the_host():
             enc.set_subsampling(dict(sp, lin_w=sp["lin_w"][:, :-1]))
     finally:
         enc.free()
+
+
+def test_kernel_override_is_explicit_and_checked():
+    """Kernel choices are forced only through vx_set_kernel_override (the library reads no environment variable):
+    known names and values are taken and cleared, anything else is refused with VX_ERR_INVALID."""
+    import subprocess
+
+    L = vx.lib()
+    for name, value in [("gemm", b"stream"), ("gemm", b"small"), ("tile", b"2x4"), ("small_tile", b"1x8"),
+                        ("stream_grid", b"16")]:
+        assert L.vx_set_kernel_override(name.encode(), value) == 0
+        assert L.vx_set_kernel_override(name.encode(), None) == 0
+    for name, value in [(b"gemm", b"fastest"), (b"tile", b"2by4"), (b"stream_grid", b"12"), (b"grid", b"8")]:
+        assert L.vx_set_kernel_override(name, value) == kernels.VX_ERR_INVALID
+    with kernels.kernel_override(gemm="direct", tile="1x2"):
+        pass
+    so = os.path.join(ROOT, "voxrt_amd", "libvoxrt_hip.so")
+    strings = subprocess.run(["strings", so], capture_output=True, text=True).stdout
+    assert "VX_GEMM" not in strings and "VX_STREAM_GRID" not in strings and "VX_SMALL_TILE" not in strings

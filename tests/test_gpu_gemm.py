@@ -385,6 +385,35 @@ def test_large_token_kernel_ranges_with_nan_canary(dev, orc):
         _assert_bits_equal(got[inside], want[inside], f"rows {r0}..{r1} toks {t0}..{t1}")
 
 
+@pytest.mark.parametrize("m,k,n_out,grid", [(1536 + 37, 1024, 1024, 8), (1024, 4096, 1024, 8), (338, 1024, 4096, 0)])
+def test_group_sums_on_the_fast_kernels(dev, orc, m, k, n_out, grid):
+    """The single-GEMM workload's literal output, int32 accumulators plus fp32 dequant (one group, Store), from the
+    streaming kernel (forced grids: several tiles per workgroup; K = 1024 and 4096) and from the small-token kernel
+    (the last 37 tokens; all of M = 338): every int32 sum and every fp32 output equal to the oracle, with and
+    without bias."""
+    import torch
+
+    import voxrt_amd as vx
+
+    trits, s16, x = _workload(orc, m, k, n_out, k, seed_cfg=6)
+    ws = orc.f16_to_f32(s16)
+    w = vx.TernaryMatrix.from_packed_f32(synth.pack_rows(trits), ws, n_out, k, k)
+    q, xs, _ = orc.quantize(x, k)
+    xa = vx.QuantAct.quantize(_t(x, dev), k)
+    want, want_gs = orc.gemm(trits, ws, q, xs, k, want_group_sums=True)
+    bias = (synth.Lcg(43).take(n_out) % 100).astype(np.float32) / np.float32(10.0)
+    with vx.kernels.kernel_override(**({"gemm": "stream", "stream_grid": grid} if grid else {})):
+        for with_bias in (False, True):
+            y = torch.full((m, n_out), float("nan"), dtype=torch.float32, device=dev)
+            gs = torch.full((1, m, n_out), -7, dtype=torch.int32, device=dev)
+            vx.gemm_ep(w, xa, y, _t(bias, dev) if with_bias else None, vx.Epilogue.Store, gs)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(gs.cpu().numpy(), want_gs, err_msg=f"group sums {m}x{k}x{n_out}")
+            exp = (want + bias[None, :]).astype(np.float32) if with_bias else want
+            _assert_bits_equal(y.cpu().numpy(), exp, f"y with group sums {m}x{k}x{n_out} bias={with_bias}")
+    w.free()
+
+
 @pytest.mark.parametrize("m,k,n_out,grid", [(1536, 1024, 2048, 16), (1536 + 37, 1024, 1024, 8),
                                             (1024, 4096, 1024, 8), (2048, 1024, 3072, 0)])
 def test_stream_kernel_every_output(dev, orc, m, k, n_out, grid):
@@ -404,10 +433,7 @@ def test_stream_kernel_every_output(dev, orc, m, k, n_out, grid):
     rng = synth.Lcg(41)
     base = ((rng.take(m * n_out) % 200).astype(np.float32) * np.float32(0.01) - np.float32(1.0)).reshape(m, n_out)
     bias = (rng.take(n_out) % 100).astype(np.float32) / np.float32(10.0)
-    old = {v: os.environ.get(v) for v in ("VX_GEMM", "VX_STREAM_GRID")}
-    os.environ["VX_GEMM"] = "stream"
-    os.environ["VX_STREAM_GRID"] = str(grid)
-    try:
+    with vx.kernels.kernel_override(gemm="stream", stream_grid=grid or None):
         for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
             want = orc.gemm(trits, ws, q, xs, k, y=base.copy(), ep=ep_kind, alpha=alpha)
             for with_bias in (False, True):
@@ -416,12 +442,6 @@ def test_stream_kernel_every_output(dev, orc, m, k, n_out, grid):
                 exp = (want + bias[None, :]).astype(np.float32) if with_bias else want
                 _assert_bits_equal(y.cpu().numpy(), exp, f"stream {m}x{k}x{n_out} grid={grid} ep={ep_kind} "
                                                          f"bias={with_bias}")
-    finally:
-        for v, val in old.items():
-            if val is None:
-                os.environ.pop(v, None)
-            else:
-                os.environ[v] = val
 
 
 @pytest.mark.parametrize("m,k,n_out,grid", [(1536, 1024, 2048, 16), (1536 + 37, 1024, 1024, 8),
@@ -442,10 +462,7 @@ def test_stream_groups_kernel_every_output(dev, orc, m, k, n_out, grid):
     rng = synth.Lcg(43)
     base = ((rng.take(m * n_out) % 200).astype(np.float32) * np.float32(0.01) - np.float32(1.0)).reshape(m, n_out)
     bias = (rng.take(n_out) % 100).astype(np.float32) / np.float32(10.0)
-    old = {v: os.environ.get(v) for v in ("VX_GEMM", "VX_STREAM_GRID")}
-    os.environ["VX_GEMM"] = "stream"
-    os.environ["VX_STREAM_GRID"] = str(grid)
-    try:
+    with vx.kernels.kernel_override(gemm="stream", stream_grid=grid or None):
         for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
             want = orc.gemm(trits, ws, q, xs, group, y=base.copy(), ep=ep_kind, alpha=alpha)
             for with_bias in (False, True):
@@ -454,12 +471,6 @@ def test_stream_groups_kernel_every_output(dev, orc, m, k, n_out, grid):
                 exp = (want + bias[None, :]).astype(np.float32) if with_bias else want
                 _assert_bits_equal(y.cpu().numpy(), exp, f"stream groups {m}x{k}x{n_out} grid={grid} "
                                                          f"ep={ep_kind} bias={with_bias}")
-    finally:
-        for v, val in old.items():
-            if val is None:
-                os.environ.pop(v, None)
-            else:
-                os.environ[v] = val
 
 
 @pytest.mark.parametrize("tile,group,m,k", [
@@ -487,10 +498,7 @@ def test_small_kernel_every_output(dev, orc, tile, group, m, k):
     rng = synth.Lcg(47)
     base = ((rng.take(m * n_out) % 200).astype(np.float32) * np.float32(0.01) - np.float32(1.0)).reshape(m, n_out)
     bias = (rng.take(n_out) % 100).astype(np.float32) / np.float32(10.0)
-    old = {v: os.environ.get(v) for v in ("VX_GEMM", "VX_SMALL_TILE")}
-    os.environ["VX_GEMM"] = "small"
-    os.environ["VX_SMALL_TILE"] = tile
-    try:
+    with vx.kernels.kernel_override(gemm="small", small_tile=tile):
         for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
             want = orc.gemm(trits, ws, q, xs, g, y=base.copy(), ep=ep_kind, alpha=alpha)
             for with_bias in (False, True):
@@ -499,12 +507,6 @@ def test_small_kernel_every_output(dev, orc, tile, group, m, k):
                 exp = (want + bias[None, :]).astype(np.float32) if with_bias else want
                 _assert_bits_equal(y.cpu().numpy(), exp, f"small tile={tile} G={g} {m}x{k}x{n_out} ep={ep_kind} "
                                                          f"bias={with_bias}")
-    finally:
-        for v, val in old.items():
-            if val is None:
-                os.environ.pop(v, None)
-            else:
-                os.environ[v] = val
 
 
 @pytest.mark.parametrize("m,k,n_out,group,ep_kind,with_bias", [

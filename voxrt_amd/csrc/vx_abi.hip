@@ -47,6 +47,7 @@ void *static_attn_ws();
 void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
                         const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
                         hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t, int64_t rel_ld);
+void set_kernel_override(const char *name, const char *value);
 vx_encoder *encoder_create(const vx_encoder_config *cfg);
 void encoder_free(vx_encoder *e);
 void encoder_use_graphs(vx_encoder *e, bool on);
@@ -122,6 +123,10 @@ vx_status vx_init(int device) {
         vx::hip_check(hipSetDevice(device), "hipSetDevice");
         (void)vx::static_attn_ws();  // the device address of the workspace-free attention core's array
     });
+}
+
+vx_status vx_set_kernel_override(const char *name, const char *value) {
+    return guarded([&] { vx::set_kernel_override(name, value); });
 }
 
 vx_status vx_shutdown(void) {

@@ -2,6 +2,7 @@
 // vx_gemm_stream.hip, vx_gemm_stream_g.hip, vx_gemm_small.hip).
 #pragma once
 
+#include <atomic>
 #include <type_traits>
 
 #include "vx_internal.h"
@@ -65,6 +66,15 @@ __device__ __forceinline__ void static_for(F &&f) {
         static_for<B + 1, E>(f);
     }
 }
+
+// Kernel choices forced by vx_set_kernel_override (tests and tuning; nothing is forced by default and no environment
+// variable is read): the GEMM kernel family, the tile of the split-K / direct / LDS kernels and of the small-token
+// kernel (16 * mt tokens x 16 * nt rows, encoded mt * 16 + nt), and the streaming kernels' grid (workgroups).
+enum ForcedKernel { kForceNone, kForceDirect, kForceSplitK, kForceLds, kForceBig, kForceSplitG, kForceSmall, kForceStream };
+struct KernelOverrides {
+    std::atomic<int> gemm{kForceNone}, tile{0}, small_tile{0}, stream_grid{0};
+};
+KernelOverrides &overrides();
 
 // The streaming kernels run the GEMM and return true when the shape and window fit them (whole 128-token x
 // 256-row tiles of a full-width ternary GEMM), else return false and launch nothing.

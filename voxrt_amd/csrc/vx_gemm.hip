@@ -1128,7 +1128,7 @@ int64_t wgs_of(const GemmArgs &a, int bm, int bn) {
 // Kernel and tile per shape. One group (G = K) with up to 1024 tokens and K a multiple of 256 takes the split-K
 // kernel; the large-token ternary shapes whose K is a multiple of 512 the LDS-staged kernel; everything else the
 // direct kernel (one group, or 64 or 128 columns per group) or, for other group sizes, the LDS-staged kernel with
-// one stage in flight. VX_GEMM=direct|splitk|lds and VX_TILE=MTxNT override (tuning).
+// one stage in flight. vx_set_kernel_override("gemm" / "tile") forces a kernel and a tile (tests, tuning).
 Plan plan_for(const GemmArgs &a, bool tern, bool gs, bool single) {
     const bool direct_ok = single || a.spg == 1 || a.spg == 2;
     const bool splitk_ok = single && (a.inp / 64) % 4 == 0;
@@ -1142,22 +1142,18 @@ Plan plan_for(const GemmArgs &a, bool tern, bool gs, bool single) {
                 : (big_ok && m > 1024)     ? kBig
                 : (lds_fast_ok && m > 1024) ? kLds
                                             : kDirect;
-    const char *kv = getenv("VX_GEMM");
-    if (kv && *kv) {
-        if (!strcmp(kv, "lds") && lds_fast_ok) kind = kLds;
-        if (!strcmp(kv, "direct") && direct_ok) kind = kDirect;
-        if (!strcmp(kv, "splitk") && splitk_ok) kind = kSplitK;
-        if (!strcmp(kv, "big") && big_ok) kind = kBig;
-        if (!strcmp(kv, "splitg") && splitg_ok) kind = kSplitG;
-    }
+    const int forced = overrides().gemm.load(std::memory_order_relaxed);
+    if (forced == kForceLds && lds_fast_ok) kind = kLds;
+    if (forced == kForceDirect && direct_ok) kind = kDirect;
+    if (forced == kForceSplitK && splitk_ok) kind = kSplitK;
+    if (forced == kForceBig && big_ok) kind = kBig;
+    if (forced == kForceSplitG && splitg_ok) kind = kSplitG;
+    const int ft = overrides().tile.load(std::memory_order_relaxed), fmt = ft >> 4, fnt = ft & 15;
     if (kind == kBig) return Plan{kBig, 8, 4};
     if (kind == kSplitG) {
         static const Plan gtiles[] = {{kSplitG, 1, 8}, {kSplitG, 2, 4}, {kSplitG, 4, 2}};
-        const char *ge = getenv("VX_TILE");
-        int gm = 0, gn = 0;
-        if (ge && *ge && sscanf(ge, "%dx%d", &gm, &gn) == 2)
-            for (const Plan &t : gtiles)
-                if (gm == t.mt && gn == t.nt) return t;
+        for (const Plan &t : gtiles)
+            if (fmt == t.mt && fnt == t.nt) return t;
         return gtiles[0];
     }
     static const Plan dtiles[] = {{kDirect, 4, 4}, {kDirect, 2, 4}, {kDirect, 2, 2}, {kDirect, 1, 2}, {kDirect, 1, 1}};
@@ -1165,12 +1161,8 @@ Plan plan_for(const GemmArgs &a, bool tern, bool gs, bool single) {
     static const Plan stiles[] = {{kSplitK, 2, 4}, {kSplitK, 1, 8}, {kSplitK, 4, 2}};
     const Plan *tiles = kind == kDirect ? dtiles : kind == kLds ? ltiles : stiles;
     const int ntiles = kind == kDirect ? 5 : 3;
-    const char *env = getenv("VX_TILE");
-    int emt = 0, ent = 0;
-    if (env && *env && sscanf(env, "%dx%d", &emt, &ent) == 2) {
-        for (int i = 0; i < ntiles; i++)
-            if (tiles[i].mt == emt && tiles[i].nt == ent) return tiles[i];
-    }
+    for (int i = 0; i < ntiles; i++)
+        if (tiles[i].mt == fmt && tiles[i].nt == fnt) return tiles[i];
     if (kind == kLds) return m >= 4096 ? ltiles[1] : ltiles[2];
     if (kind == kSplitK) return stiles[0];
     for (int i = 0; i < ntiles; i++)
@@ -1301,9 +1293,11 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
     GemmArgs a = gemm_args(w, xq, xs_t, xg_t, n, y, bias, ep, alpha, gs, r0, r1, t0, t1, true);
     if (r0 == r1 || t0 == t1) return;
     const bool tern = w->ternary, g = gs != nullptr, single = w->ng == 1;
+    // the streaming and small-token kernels also write the group sums of one group with the Store epilogue
+    const bool fast_ok = !g || (single && ep == VX_EP_STORE);
     // whole 128-token tiles of a full-width ternary GEMM (one group or 128-column groups): the streaming kernels;
     // the remaining tokens (fewer than 128) go through the kernels below
-    if (tern && !g && r0 == 0 && r1 == w->out && t0 == 0 && n >= 128) {
+    if (tern && fast_ok && r0 == 0 && r1 == w->out && t0 == 0 && n >= 128) {
         const int64_t full = n / 128 * 128;
         if (full < (1ll << 30) && (single ? gemm_stream(a, (int)full, st) : gemm_stream_groups(a, (int)full, st))) {
             if (full == n) return;
@@ -1311,7 +1305,7 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
             a.m_base = full;
         }
     }
-    if (tern && !g && gemm_small(a, st)) return;
+    if (tern && fast_ok && gemm_small(a, st)) return;
     const Plan p = plan_for(a, tern, g, single);
     if (p.kind == kBig) {
         const dim3 grid((unsigned)((a.r1 - a.n_base + 255) / 256), (unsigned)((a.t1 - a.m_base + 127) / 128));
@@ -1359,6 +1353,44 @@ void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_
 
 void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const float *g, const float *b, int8_t *q,
                  float *scales_t, int32_t *gsum_t, hipStream_t stream);
+
+KernelOverrides &overrides() {
+    static KernelOverrides o;
+    return o;
+}
+
+// vx_set_kernel_override: name "gemm" (direct, splitk, lds, big, splitg, small, stream), "tile" and "small_tile"
+// ("MTxNT"), "stream_grid" (workgroups, a multiple of 8); NULL or "" clears the name's override.
+void set_kernel_override(const char *name, const char *value) {
+    require(name != nullptr, "override name must not be NULL");
+    const std::string n(name), v(value ? value : "");
+    KernelOverrides &o = overrides();
+    auto tile_code = [&](const std::string &t) {
+        int mt = 0, nt = 0;
+        require(sscanf(t.c_str(), "%dx%d", &mt, &nt) == 2 && mt > 0 && mt < 16 && nt > 0 && nt < 16,
+                "a tile override is MTxNT with 0 < MT, NT < 16");
+        return mt * 16 + nt;
+    };
+    if (n == "gemm") {
+        static const char *kinds[] = {"", "direct", "splitk", "lds", "big", "splitg", "small", "stream"};
+        for (int k = 0; k < 8; k++)
+            if (v == kinds[k]) {
+                o.gemm.store(k, std::memory_order_relaxed);
+                return;
+            }
+        throw Error(VX_ERR_INVALID, "unknown gemm override '" + v + "'");
+    } else if (n == "tile") {
+        o.tile.store(v.empty() ? 0 : tile_code(v), std::memory_order_relaxed);
+    } else if (n == "small_tile") {
+        o.small_tile.store(v.empty() ? 0 : tile_code(v), std::memory_order_relaxed);
+    } else if (n == "stream_grid") {
+        const int g = v.empty() ? 0 : atoi(v.c_str());
+        require(g == 0 || (g >= 8 && g % 8 == 0), "stream_grid is a positive multiple of 8");
+        o.stream_grid.store(g, std::memory_order_relaxed);
+    } else {
+        throw Error(VX_ERR_INVALID, "unknown override name '" + n + "'");
+    }
+}
 
 // The FFN up-projection with the down-projection's quantization fused (encoder.rs:87-89: forward_prepared_ep with
 // Silu into hbuf, then prepare(hbuf) = QuantAct::quantize_layout, packed.rs:307-436): y = ep(x . w^T) (+ bias),

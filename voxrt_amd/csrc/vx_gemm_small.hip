@@ -19,6 +19,9 @@
 // output rows of (16 * MT * NT / 32) tokens: for one group it adds the four partial sums and folds once; with
 // groups it folds the chunk's four group sums in ascending group order after every chunk.
 //
+// Group-sum output (one group, Store): the exact int32 sums S (the fold's operand) are also stored, to the
+// group_sums buffer [1][n][out], beside y.
+//
 // Quantized output (16 x 128 tiles): instead of y, the epilogue writes the next GEMM's activations. The 16 fold
 // threads of a token hold its 128 outputs of one 128-column group after the epilogue and bias, so the group's
 // quantization (QuantAct::quantize_group, packed.rs:527-535: amax, s = amax / 127 or 1, inv = 1 / s, codes
@@ -38,9 +41,10 @@ constexpr int kMaxG = 32;  // groups staged in LDS (K <= 4096 with 128-column gr
 // MAXG: groups the LDS scale tables hold (8 or 32; sized so that a small K leaves room for more workgroups per CU).
 // 16 x 128 tiles with a ring of at most 4 steps (one group, or a quantized output) are held to 168 registers, so
 // that three workgroups fit per CU and a T = 338 grid of 704 tiles runs in one round.
-template <int MT, int NT, bool GROUPED, int D, int EP, bool BIAS, bool QOUT, int MAXG>
+template <int MT, int NT, bool GROUPED, int D, int EP, bool BIAS, bool QOUT, int MAXG, bool GSO = false>
 __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || QOUT)) ? 3 : 1) void tgemm_small_kernel(
     const GemmArgs a, const int n_mt, const int per_xcd, const int ntiles) {
+    static_assert(!GSO || (!GROUPED && !QOUT && EP == VX_EP_STORE), "group sums: one group, Store epilogue");
     constexpr int BM = 16 * MT, BN = 16 * NT, BNP = BN + 4;  // BNP: LDS row pitch (16-byte shift per token row)
     constexpr int TPR = BN / 8;                               // fold threads per token row
     constexpr int RPP = 256 / TPR;                            // token rows per fold pass
@@ -74,6 +78,7 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
     const auto wsrs = make_rsrc(a.ws_t, a.ws_bytes);
     const auto yrs = make_rsrc(a.y, a.y_bytes);
     const auto brs = make_rsrc(a.bias, BIAS ? (uint32_t)(a.out * 4) : 0u);
+    const auto gsrs = make_rsrc(a.gs, GSO ? a.y_bytes : 0u);  // [1][n][out] int32, the same layout as y
 
     // fold ownership: token rows tt0 + r * RPP of the tile, output rows c0 .. c0 + 7
     const int tt0 = tid / TPR, c0 = (tid % TPR) * 8, o0 = n0 + c0;
@@ -156,6 +161,7 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int j = 0; j < 8; j++) accf[r][j] = 0.0f;
+    v4i gso[GSO ? R : 1][2];  // the exact sums of the group-sum output
 
     // int32 sums of this wavefront -> its LDS plane (one 16-byte write per block)
     auto to_lds = [&](int buf) __attribute__((always_inline)) {
@@ -260,6 +266,10 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
             }
 #pragma unroll
             for (int j = 0; j < 8; j++) accf[r][j] = __builtin_fmaf((float)S[j], xsr[r] * wsv[j], 0.0f);
+            if constexpr (GSO) {
+                gso[r][0] = v4i{S[0], S[1], S[2], S[3]};
+                gso[r][1] = v4i{S[4], S[5], S[6], S[7]};
+            }
         }
     }
 
@@ -316,6 +326,10 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
             const uint32_t so = (uint32_t)t * out4 + (uint32_t)o0 * 4;
             __builtin_amdgcn_raw_buffer_store_b128(lo, yrs, so, 0, 0);
             __builtin_amdgcn_raw_buffer_store_b128(hi, yrs, so + 16, 0, 0);
+            if constexpr (GSO) {
+                __builtin_amdgcn_raw_buffer_store_b128(gso[r][0], gsrs, so, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(gso[r][1], gsrs, so + 16, 0, 0);
+            }
         }
     }
 }
@@ -376,6 +390,14 @@ void launch_small_g(const GemmArgs &a, int grid, int n_mt, int per_xcd, int ntil
           : tgemm_small_kernel<MT, NT, GROUPED, D, EP, false, true, MAXG>)
             auto k = a.ep == VX_EP_SILU ? VX_SMALLQ(VX_EP_SILU) : VX_SMALLQ(VX_EP_STORE);
 #undef VX_SMALLQ
+            k<<<grid, 256, 0, st>>>(a, n_mt, per_xcd, ntiles);
+            return;
+        }
+    }
+    if constexpr (!GROUPED) {
+        if (a.gs) {  // group sums (one group): Store only
+            auto k = bias ? tgemm_small_kernel<MT, NT, false, D, VX_EP_STORE, true, false, MAXG, true>
+                          : tgemm_small_kernel<MT, NT, false, D, VX_EP_STORE, false, false, MAXG, true>;
             k<<<grid, 256, 0, st>>>(a, n_mt, per_xcd, ntiles);
             return;
         }
@@ -442,18 +464,19 @@ bool gemm_small(const GemmArgs &a, hipStream_t st) {
         hip_check(hipGetLastError(), "tgemm_small launch");
         return true;
     }
-    if (a.gs != nullptr || a.y_bytes == 0 || !a.vec_ok) return false;
+    // group sums only with one group and the Store epilogue (other cases: the kernels of vx_gemm.hip)
+    if (a.gs != nullptr && (grouped || a.ep != VX_EP_STORE)) return false;
+    if (a.y_bytes == 0 || !a.vec_ok) return false;
     if (a.r0 != 0 || a.r1 != a.out || a.n_base != 0) return false;
     if (grouped ? (a.spg != 2 || a.ng % 4 != 0 || a.ng > kMaxG) : (a.inp / 64) % 4 != 0) return false;
-    // VX_GEMM=small forces this kernel (=stream keeps it for the tokens after the streaming kernel's tiles; any
-    // other value turns it off); VX_SMALL_TILE=MTxNT forces a tile (tests and tuning)
-    const char *kv = getenv("VX_GEMM");
-    if (kv && *kv && strcmp(kv, "small") != 0 && strcmp(kv, "stream") != 0) return false;
-    int fm = 0, fn = 0;
-    const char *tv = getenv("VX_SMALL_TILE");
-    if (tv && *tv && sscanf(tv, "%dx%d", &fm, &fn) != 2) fm = fn = 0;
+    // a "small" override forces this kernel ("stream" keeps it for the tokens after the streaming kernel's tiles; any
+    // other kernel override turns it off); a "small_tile" override forces a tile (tests and tuning)
+    const int forced = overrides().gemm.load(std::memory_order_relaxed);
+    if (forced != kForceNone && forced != kForceSmall && forced != kForceStream) return false;
+    const int ft = overrides().small_tile.load(std::memory_order_relaxed);
+    const int fm = ft >> 4, fn = ft & 15;
     // up to 1024 tokens; longer token ranges go to the kernels built for throughput
-    if (a.t1 - a.m_base > 1024 && !(kv && strcmp(kv, "small") == 0)) return false;
+    if (a.t1 - a.m_base > 1024 && forced != kForceSmall) return false;
     const SmallPlan p = plan_small(a, grouped, fm, fn);
     if (p.mt == 0) return false;
     const int64_t ntok = a.t1 - a.m_base;

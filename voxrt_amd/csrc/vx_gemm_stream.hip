@@ -56,8 +56,11 @@ constexpr int kValuPerDs = 2;    // VALU instructions placed beside each fragmen
 constexpr int kValuPerMfma = 3;  // VALU instructions after each remaining MFMA (one MFMA is 16 cycles)
 __device__ constexpr int wait_of(int pd, int i, int nk) { return 2 + 5 * (pd - 2) + ((i >= nk - pd + 1) ? 4 : 0); }
 
-template <int EP, bool BIAS, bool K16, bool OCC2>
+template <int EP, bool BIAS, bool K16, bool OCC2, bool GSO>
 __global__ __launch_bounds__(256, OCC2 ? 2 : 1) void tgemm_stream_kernel(const GemmArgs a, const StreamGeom g) {
+    // GSO: the exact int32 sums S are stored too, to the group-sum buffer [1][n][out] (Store epilogue; each tile's
+    // epilogue after its last step)
+    static_assert(!GSO || (EP == VX_EP_STORE && !OCC2), "group sums: Store epilogue");
     // OCC2: two workgroups per CU (two wavefronts per SIMD), each with half the LDS ring and one accumulator set, so
     // that one workgroup's epilogue, waits and barriers overlap the other's MFMAs
     constexpr int kPD = OCC2 ? 3 : 6;  // steps the loads run ahead
@@ -66,7 +69,7 @@ __global__ __launch_bounds__(256, OCC2 ? 2 : 1) void tgemm_stream_kernel(const G
     // SiLU (its VALU work made the steps of the next tile VALU-bound: 67 -> 62 us for FFN-up) and for K > 1024
     // (FFN-down 32.7 -> 31.4 us); the Store epilogue with K = 1024 keeps the two-blocks-per-step overlap
     // (40 us against 43).
-    constexpr bool DRAIN = OCC2 || EP != VX_EP_STORE || !K16;
+    constexpr bool DRAIN = OCC2 || GSO || EP != VX_EP_STORE || !K16;
     typedef __attribute__((address_space(3))) void lds_void;
     // one LDS object per activation slot and per scale table: the compiler then sees that a DMA into one slot
     // does not alias the fragment reads of another and adds no vmcnt wait of its own before them
@@ -109,6 +112,7 @@ __global__ __launch_bounds__(256, OCC2 ? 2 : 1) void tgemm_stream_kernel(const G
     const auto wsrs = make_rsrc(a.ws_t, a.ws_bytes);
     const auto brs = make_rsrc(a.bias, BIAS ? (uint32_t)(a.out * 4) : 0u);
     const auto yrs = make_rsrc(a.y, a.y_bytes);
+    const auto gsrs = make_rsrc(a.gs, GSO ? a.y_bytes : 0u);
 
     // activation DMA: this wave fills token blocks 2w, 2w+1 of the tile; lane l -> row l/4 of the block, LDS
     // position l%4, global chunk (l%4) ^ ((row >> 2) & 3). The tile's token base travels in the scalar offset
@@ -225,10 +229,11 @@ __global__ __launch_bounds__(256, OCC2 ? 2 : 1) void tgemm_stream_kernel(const G
         }
         const float wsv[4] = {ws.x, ws.y, ws.z, ws.w}, bv[4] = {bia.x, bia.y, bia.z, bia.w},
                     ov[4] = {old.x, old.y, old.z, old.w};
-        v4i r;
+        v4i r, sums;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const float v = __builtin_fmaf((float)(acc[tb][ob][e] - gsum), xs * wsv[e], 0.0f);
+            sums[e] = acc[tb][ob][e] - gsum;
+            const float v = __builtin_fmaf((float)sums[e], xs * wsv[e], 0.0f);
             float res = v;
             if constexpr (EP == VX_EP_SILU) res = silu_fast(v);
             if constexpr (EP == VX_EP_ADD_SCALED) res = __builtin_fmaf(a.alpha, v, ov[e]);
@@ -236,6 +241,7 @@ __global__ __launch_bounds__(256, OCC2 ? 2 : 1) void tgemm_stream_kernel(const G
             r[e] = __float_as_int(res);
         }
         __builtin_amdgcn_raw_buffer_store_b128(r, yrs, vy, so, 0);
+        if constexpr (GSO) __builtin_amdgcn_raw_buffer_store_b128(sums, gsrs, vy, so, 0);
     };
 
     // one K step. i: tile step (runtime in the middle loop); SLOT = i % 8 (LDS slot);
@@ -449,10 +455,19 @@ __global__ __launch_bounds__(256, OCC2 ? 2 : 1) void tgemm_stream_kernel(const G
 
 template <int EP, bool BIAS>
 void launch_stream(const GemmArgs &a, const StreamGeom &g, int grid, hipStream_t st) {
+    if constexpr (EP == VX_EP_STORE) {
+        if (a.gs) {
+            if (g.nk == 16)
+                tgemm_stream_kernel<EP, BIAS, true, false, true><<<grid, 256, 0, st>>>(a, g);
+            else
+                tgemm_stream_kernel<EP, BIAS, false, false, true><<<grid, 256, 0, st>>>(a, g);
+            return;
+        }
+    }
     if (g.nk == 16)
-        tgemm_stream_kernel<EP, BIAS, true, occ2_of(EP, true)><<<grid, 256, 0, st>>>(a, g);
+        tgemm_stream_kernel<EP, BIAS, true, occ2_of(EP, true), false><<<grid, 256, 0, st>>>(a, g);
     else
-        tgemm_stream_kernel<EP, BIAS, false, occ2_of(EP, false)><<<grid, 256, 0, st>>>(a, g);
+        tgemm_stream_kernel<EP, BIAS, false, occ2_of(EP, false), false><<<grid, 256, 0, st>>>(a, g);
 }
 
 }  // namespace
@@ -475,11 +490,11 @@ int cu_count() {
 
 bool gemm_stream(const GemmArgs &a, int tokens_full, hipStream_t st) {
     const int64_t nk = a.inp / 64;
-    if (a.ng != 1 || a.gs != nullptr || a.y_bytes == 0) return false;
+    if (a.ng != 1 || (a.gs != nullptr && a.ep != VX_EP_STORE) || a.y_bytes == 0) return false;
     if (a.inp % 64 != 0 || nk < 16 || nk % 8 != 0 || (nk != 16 && nk < 24)) return false;
     if (a.out % kBN != 0 || a.r0 != 0 || a.r1 != a.out || a.t0 != 0 || tokens_full % kBM != 0) return false;
-    const char *kv = getenv("VX_GEMM");
-    if (kv && *kv && strcmp(kv, "stream") != 0) return false;
+    const int forced = overrides().gemm.load(std::memory_order_relaxed);
+    if (forced != kForceNone && forced != kForceStream) return false;
     StreamGeom g;
     g.n_nt = (int)(a.out / kBN);
     g.ntiles = (tokens_full / kBM) * g.n_nt;
@@ -487,10 +502,10 @@ bool gemm_stream(const GemmArgs &a, int tokens_full, hipStream_t st) {
     g.nk = (int)nk;
     g.ng = 1;
     const int cus = cu_count();
-    if (g.ntiles < cus && !(kv && *kv)) return false;  // too few tiles to fill the chip: the other kernels
-    int per_x = std::min((occ2_of(a.ep, nk == 16) ? 2 : 1) * cus / 8, g.per_xcd);
-    const char *ge = getenv("VX_STREAM_GRID");  // workgroups (a multiple of 8): tuning and tests
-    if (ge && *ge && atoi(ge) >= 8) per_x = std::min(atoi(ge) / 8, g.per_xcd);
+    if (g.ntiles < cus && forced == kForceNone) return false;  // too few tiles to fill the chip: the other kernels
+    int per_x = std::min((occ2_of(a.ep, nk == 16) && !a.gs ? 2 : 1) * cus / 8, g.per_xcd);
+    const int fg = overrides().stream_grid.load(std::memory_order_relaxed);  // workgroups: tests and tuning
+    if (fg >= 8) per_x = std::min(fg / 8, g.per_xcd);
     const int grid = 8 * per_x;
     // XCD x's workgroup i starts at tile x*per_xcd + i; on the last XCD that tile may not exist (fewer tiles), and
     // such a workgroup returns at once

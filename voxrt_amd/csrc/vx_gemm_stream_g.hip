@@ -291,8 +291,8 @@ bool gemm_stream_groups(const GemmArgs &a, int tokens_full, hipStream_t st) {
     if (a.spg != 2 || a.ng < 2 || a.gs != nullptr || a.y_bytes == 0) return false;  // 128-column groups
     if (a.inp % 512 != 0 || nk < 16) return false;
     if (a.out % kBN != 0 || a.r0 != 0 || a.r1 != a.out || a.t0 != 0 || tokens_full % kBM != 0) return false;
-    const char *kv = getenv("VX_GEMM");
-    if (kv && *kv && strcmp(kv, "stream") != 0) return false;
+    const int forced = overrides().gemm.load(std::memory_order_relaxed);
+    if (forced != kForceNone && forced != kForceStream) return false;
     StreamGeom g;
     g.n_nt = (int)(a.out / kBN);
     g.ntiles = (tokens_full / kBM) * g.n_nt;
@@ -300,10 +300,10 @@ bool gemm_stream_groups(const GemmArgs &a, int tokens_full, hipStream_t st) {
     g.nk = (int)nk;
     g.ng = (int)a.ng;
     const int cus = cu_count();
-    if (g.ntiles < cus / 2 && !(kv && *kv)) return false;  // too few tiles: the other kernels
+    if (g.ntiles < cus / 2 && forced == kForceNone) return false;  // too few tiles: the other kernels
     int per_x = std::min(cus / 8, g.per_xcd);
-    const char *ge = getenv("VX_STREAM_GRID");  // workgroups (a multiple of 8): tuning and tests
-    if (ge && *ge && atoi(ge) >= 8) per_x = std::min(atoi(ge) / 8, g.per_xcd);
+    const int fg = overrides().stream_grid.load(std::memory_order_relaxed);  // workgroups: tests and tuning
+    if (fg >= 8) per_x = std::min(fg / 8, g.per_xcd);
     const int grid = 8 * per_x;
     GemmArgs b = a;
     b.t1 = tokens_full;

@@ -53,6 +53,7 @@ def lib() -> C.CDLL:
             "vx_detect": (I, []),
             "vx_init": (I, [I]),
             "vx_shutdown": (I, []),
+            "vx_set_kernel_override": (I, [C.c_char_p, C.c_char_p]),
             "vx_tmat_upload_packed": (I, [P, P, I64, I64, I64, C.POINTER(P)]),
             "vx_tmat_upload_packed_f32": (I, [P, P, I64, I64, I64, C.POINTER(P)]),
             "vx_tmat_upload_i8": (I, [P, P, I64, I64, I64, C.POINTER(P)]),
@@ -127,6 +128,29 @@ def kernel() -> Kernel:
     if want == "hip" and best == Kernel.Hip:
         return Kernel.Hip
     return best
+
+
+def set_kernel_override(name: str, value) -> None:
+    """Force a GEMM kernel choice (vx_set_kernel_override): gemm=direct|splitk|lds|big|splitg|small|stream,
+    tile / small_tile="MTxNT", stream_grid=<workgroups>; None or "" clears it. For tests and tuning."""
+    check(lib().vx_set_kernel_override(name.encode(), None if value in (None, "") else str(value).encode()))
+
+
+class kernel_override:
+    """Context manager: kernel_override(gemm="stream", stream_grid=8) forces those choices inside the block."""
+
+    def __init__(self, **kw):
+        self.kw = kw
+
+    def __enter__(self):
+        for k, v in self.kw.items():
+            set_kernel_override(k, v)
+        return self
+
+    def __exit__(self, *exc):
+        for k in self.kw:
+            set_kernel_override(k, None)
+        return False
 
 
 @dataclass(frozen=True)
