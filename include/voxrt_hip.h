@@ -8,6 +8,7 @@
  *   vx_tmat_upload_packed             <- TernaryMatrix::from_packed_layout (packed.rs:73-130)
  *   vx_tmat_upload_packed_f32         <- the same with f32 scales (a per-output-channel fp32 scale, as in the
  *                                        338 x 1024 x 4096 single-GEMM workload)
+ *   vx_tmat_upload_trits              <- a TernaryMatrix in the Rows layout (packed.rs:48-60: trits + f32 scales)
  *   vx_tmat_upload_i8                 <- TernaryMatrix::from_i8_rows (packed.rs:164-201)
  *   vx_tmat_free / vx_tmat_info       <- drop / the out, inp, group, ternary fields (packed.rs:48-60)
  *   vx_quantize                       <- QuantAct::quantize_layout (packed.rs:307-436, quantize_group 527-535)
@@ -96,6 +97,12 @@ vx_status vx_tmat_upload_packed(const uint8_t *qweight, const uint16_t *scales_f
 /* As vx_tmat_upload_packed with float32 scales [out, inp/group]. */
 vx_status vx_tmat_upload_packed_f32(const uint8_t *qweight, const float *scales, int64_t out, int64_t inp,
                                     int64_t group, vx_tmat **w);
+
+/* A ternary matrix already unpacked to trits: int8 rows [out, inp] in {-1, 0, +1} (TernaryMatrix::w in the Rows
+ * layout) with float32 scales [out, inp/group]. Uploaded as a ternary matrix (the 2-bit layout, as from the model
+ * file's rows); any other value is refused with VX_ERR_INVALID. */
+vx_status vx_tmat_upload_trits(const int8_t *trits, const float *scales, int64_t out, int64_t inp, int64_t group,
+                               vx_tmat **w);
 
 /* from_i8_rows: arbitrary int8 rows [out, inp] with float32 scales [out, inp/group] (not ternary). */
 vx_status vx_tmat_upload_i8(const int8_t *rows, const float *scales, int64_t out, int64_t inp, int64_t group,

@@ -128,3 +128,13 @@ def test_kernel_override_is_explicit_and_checked():
     so = os.path.join(ROOT, "voxrt_amd", "libvoxrt_hip.so")
     strings = subprocess.run(["strings", so], capture_output=True, text=True).stdout
     assert "VX_GEMM" not in strings and "VX_STREAM_GRID" not in strings and "VX_SMALL_TILE" not in strings
+
+
+def test_trit_upload_refuses_non_trits():
+    """vx_tmat_upload_trits checks every value on the host before any device work: a 2 is refused."""
+    rows = np.zeros((4, 128), np.int8)
+    rows[2, 77] = 2
+    scales = np.ones((4, 1), np.float32)
+    h = C.c_void_p()
+    st = vx.lib().vx_tmat_upload_trits(rows.ctypes.data, scales.ctypes.data, 4, 128, 128, C.byref(h))
+    assert st == kernels.VX_ERR_INVALID and b"-1, 0 or +1 (row 2)" in vx.lib().vx_last_error()

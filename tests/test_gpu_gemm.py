@@ -615,3 +615,33 @@ def test_wrappers_refuse_tensors_of_the_wrong_shape(dev):
     torch.cuda.synchronize()
     assert bool((y == 3.0).all())
     w.free()
+
+
+def test_trit_rows_upload_equals_packed_upload(dev, orc):
+    """A matrix uploaded from unpacked trits (vx_tmat_upload_trits, the Rows layout a CPU-side TernaryMatrix holds)
+    is the same device matrix as the one uploaded from the model file's packed rows: equal outputs, bit for bit,
+    for 128-column groups and for one group, including a K whose last byte holds pad digits."""
+    import torch
+
+    import voxrt_amd as vx
+
+    rng = synth.Lcg(91)
+    for out, inp, group in [(256, 1024, 128), (384, 640, 640)]:
+        qw, s16, trits = synth.ref_random_matrix(rng, out, inp, 128)
+        ws = orc.f16_to_f32(s16)
+        if group != 128:
+            ws = ws[:, :1].copy()
+        x = synth.ref_acts(rng, 45, inp)
+        a = vx.TernaryMatrix.from_packed_f32(qw, ws, out, inp, group)
+        b = vx.TernaryMatrix.from_trits(trits, ws, out, inp, group)
+        xa = vx.QuantAct.quantize(_t(x, dev), group)
+        ya = torch.zeros((45, out), dtype=torch.float32, device=dev)
+        yb = torch.zeros((45, out), dtype=torch.float32, device=dev)
+        vx.gemm_ep(a, xa, ya, None, vx.Epilogue.Silu)
+        vx.gemm_ep(b, xa, yb, None, vx.Epilogue.Silu)
+        torch.cuda.synchronize()
+        _assert_bits_equal(yb.cpu().numpy(), ya.cpu().numpy(), f"trit upload {out}x{inp} G={group}")
+        q, xs, _ = orc.quantize(x, group)
+        _assert_bits_equal(yb.cpu().numpy(), orc.gemm(trits, ws, q, xs, group, ep=orc.EP_SILU), "against the oracle")
+        a.free()
+        b.free()

@@ -11,6 +11,7 @@ namespace vx {
 vx_tmat *upload_packed(const uint8_t *qweight, const void *scales, bool scales_f16, int64_t out, int64_t inp,
                        int64_t group);
 vx_tmat *upload_i8(const int8_t *rows, const float *scales, int64_t out, int64_t inp, int64_t group);
+vx_tmat *upload_trits(const int8_t *trits, const float *scales, int64_t out, int64_t inp, int64_t group);
 void free_tmat(vx_tmat *h);
 void quantize(const float *x, int64_t n, int64_t inp, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t,
               hipStream_t stream);
@@ -148,6 +149,15 @@ vx_status vx_tmat_upload_packed_f32(const uint8_t *qweight, const float *scales,
         vx::require(w != nullptr, "output handle pointer must not be NULL");
         *w = nullptr;
         *w = vx::upload_packed(qweight, scales, false, out, inp, group);
+    });
+}
+
+vx_status vx_tmat_upload_trits(const int8_t *trits, const float *scales, int64_t out, int64_t inp, int64_t group,
+                               vx_tmat **w) {
+    return guarded([&] {
+        vx::require(w != nullptr, "output handle pointer must not be NULL");
+        *w = nullptr;
+        *w = vx::upload_trits(trits, scales, out, inp, group);
     });
 }
 

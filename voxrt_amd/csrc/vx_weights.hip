@@ -170,6 +170,36 @@ vx_tmat *upload_packed(const uint8_t *qweight, const void *scales, bool scales_f
     return h;
 }
 
+// A TernaryMatrix already unpacked to trits (int8 rows in {-1, 0, +1}, packed.rs:48-60 in the Rows layout) with f32
+// scales: packed back into the model file's base-3 rows on the host (5 trits per byte, least significant digit
+// first, digit = trit + 1, pad digits 0: trits.rs:30-41) and uploaded through the same device repack, so the device
+// matrix is the ternary 2-bit one. A value outside {-1, 0, +1} is refused.
+vx_tmat *upload_trits(const int8_t *trits, const float *scales, int64_t out, int64_t inp, int64_t group) {
+    check_shape(out, inp, group);
+    require(trits && scales, "trits and scales must not be NULL");
+    const int64_t rb = (inp + 4) / 5;
+    std::vector<uint8_t> packed((size_t)(out * rb), 0);
+    for (int64_t o = 0; o < out; o++) {
+        const int8_t *row = trits + o * inp;
+        uint8_t *dst = packed.data() + o * rb;
+        for (int64_t b = 0; b < rb; b++) {
+            int v = 0;
+            for (int d = 4; d >= 0; d--) {
+                const int64_t c = b * 5 + d;
+                int digit = 0;
+                if (c < inp) {
+                    const int t = row[c];
+                    require(t >= -1 && t <= 1, "trits must be -1, 0 or +1 (row " + std::to_string(o) + ")");
+                    digit = t + 1;
+                }
+                v = v * 3 + digit;
+            }
+            dst[b] = (uint8_t)v;
+        }
+    }
+    return upload_packed(packed.data(), scales, false, out, inp, group);
+}
+
 vx_tmat *upload_i8(const int8_t *rows, const float *scales, int64_t out, int64_t inp, int64_t group) {
     check_shape(out, inp, group);
     require(rows && scales, "rows and scales must not be NULL");

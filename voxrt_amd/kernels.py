@@ -57,6 +57,7 @@ def lib() -> C.CDLL:
             "vx_tmat_upload_packed": (I, [P, P, I64, I64, I64, C.POINTER(P)]),
             "vx_tmat_upload_packed_f32": (I, [P, P, I64, I64, I64, C.POINTER(P)]),
             "vx_tmat_upload_i8": (I, [P, P, I64, I64, I64, C.POINTER(P)]),
+            "vx_tmat_upload_trits": (I, [P, P, I64, I64, I64, C.POINTER(P)]),
             "vx_tmat_free": (None, [P]),
             "vx_tmat_info": (I, [P, C.POINTER(I64), C.POINTER(I64), C.POINTER(I64), C.POINTER(I)]),
             "vx_quantize": (I, [P, I64, I64, I64, P, P, P, P]),
@@ -234,6 +235,18 @@ class TernaryMatrix:
             raise ValueError("qweight/scales sizes do not match out, inp, group")
         h = C.c_void_p()
         check(lib().vx_tmat_upload_packed_f32(_np_ptr(q), _np_ptr(s), out, inp, group, C.byref(h)))
+        return cls(h, out, inp, group, True)
+
+    @classmethod
+    def from_trits(cls, trits, scales, out: int, inp: int, group: int) -> "TernaryMatrix":
+        """An unpacked ternary matrix: int8 rows [out, inp] in {-1, 0, +1} with float32 scales [out, inp/group]
+        (TernaryMatrix in the Rows layout, packed.rs:48-60), uploaded as ternary (2-bit layout)."""
+        r = np.ascontiguousarray(trits, np.int8)
+        s = np.ascontiguousarray(scales, np.float32)
+        if r.size != out * inp or s.size != out * (inp // max(group, 1)):
+            raise ValueError("trits/scales sizes do not match out, inp, group")
+        h = C.c_void_p()
+        check(lib().vx_tmat_upload_trits(_np_ptr(r), _np_ptr(s), out, inp, group, C.byref(h)))
         return cls(h, out, inp, group, True)
 
     @classmethod
