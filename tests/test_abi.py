@@ -138,3 +138,40 @@ def test_trit_upload_refuses_non_trits():
     h = C.c_void_p()
     st = vx.lib().vx_tmat_upload_trits(rows.ctypes.data, scales.ctypes.data, 4, 128, 128, C.byref(h))
     assert st == kernels.VX_ERR_INVALID and b"-1, 0 or +1 (row 2)" in vx.lib().vx_last_error()
+
+
+def _c_params(text):
+    """{function: parameter count} of the vx_ functions a C header declares."""
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(vx_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_rust_bindings_declare_every_entry_point_with_its_arity():
+    """The Rust -sys crate (voxrt_amd/rust/voxrt-hip-sys/src/lib.rs, not compiled here: no cargo) declares every
+    function of include/voxrt_hip.h with the same number of parameters, and the Rust build script compiles exactly
+    the sources the Python build compiles."""
+    hdr = _c_params(open(os.path.join(ROOT, "include", "voxrt_hip.h")).read())
+    rs = open(os.path.join(ROOT, "voxrt_amd", "rust", "voxrt-hip-sys", "src", "lib.rs")).read()
+    decl = {}
+    for m in re.finditer(r"pub fn (vx_[a-z0-9_]+)\s*\((.*?)\)\s*(->[^;]*)?;", rs, flags=re.S):
+        args = re.sub(r"//[^\n]*", "", m.group(2)).strip().rstrip(",")
+        decl[m.group(1)] = 0 if not args else args.count(",") + 1
+    missing = sorted(set(hdr) - set(decl) - {"vx_npad"})
+    optional = {"vx_fold_bn", "vx_glu_dwconv_silu", "vx_glu_dwconv_silu_quantize", "vx_layer_norm", "vx_linear_f32",
+                "vx_subsampling", "vx_subsampling_scratch_floats", "vx_rel_pos_table", "vx_check_activations",
+                "vx_attention_ws_bytes", "vx_attention_core", "vx_attention_core_quantize",
+                "vx_attention_core_noalloc"}
+    assert not [n for n in missing if n not in optional], missing
+    for name, n in decl.items():
+        assert name in hdr, f"{name} is not in the header"
+        assert hdr[name] == n, f"{name}: {n} parameters in Rust, {hdr[name]} in C"
+    build_rs = open(os.path.join(ROOT, "voxrt_amd", "rust", "voxrt-hip-sys", "build.rs")).read()
+    from voxrt_amd import build as B
+
+    assert sorted(re.findall(r'"(vx_[a-z_]+\.hip)"', build_rs)) == sorted(B.SOURCES)
+    for flag in ("-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero", "-packed-fp32-ops", "--offload-arch="):
+        assert flag in build_rs
