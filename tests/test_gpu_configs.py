@@ -50,16 +50,19 @@ def _layer_set():
     return layer_shapes(338)
 
 
-@pytest.mark.parametrize("group", ["K", 128])
+@pytest.mark.parametrize("group", ["K", 128, "128ws"])
 @pytest.mark.parametrize("idx", range(9), ids=[s[0] for s in _layer_set()])
 def test_layer_linear_set_t338(dev, orc, idx, group):
     """One GEMM of the T = 338 layer set with the bench's operands (same seeds, trits, scales and activations),
-    its epilogue over a random previous y for AddScaled: every output equal to the oracle."""
+    its epilogue over a random previous y for AddScaled: every output equal to the oracle. "128ws": the model's
+    groups with the producer/consumer small-token kernel switched on."""
     import torch
 
     import voxrt_amd as vx
 
     name, m, k, n, ep, alpha = _layer_set()[idx]
+    ws_on = group == "128ws"
+    group = 128 if ws_on else group
     G = k if group == "K" else group
     ng = k // G
     role = 8 * idx
@@ -75,7 +78,8 @@ def test_layer_linear_set_t338(dev, orc, idx, group):
     xa = vx.QuantAct.quantize(torch.from_numpy(x).to(dev), G)
     y = torch.from_numpy(y0).to(dev)
     epi = {0: vx.Epilogue.Store, 1: vx.Epilogue.Silu}.get(ep) or vx.Epilogue.AddScaled(alpha)
-    vx.gemm_ep(w, xa, y, None, epi)
+    with vx.kernels.kernel_override(**({"small_ws": "on"} if ws_on else {})):
+        vx.gemm_ep(w, xa, y, None, epi)
     torch.cuda.synchronize()
     q, xs, _ = orc.quantize(x, G)
     ws = orc.f16_to_f32(s16).reshape(n, ng)

@@ -509,6 +509,64 @@ def test_small_kernel_every_output(dev, orc, tile, group, m, k):
                                                          f"bias={with_bias}")
 
 
+@pytest.mark.parametrize("m,k", [(100, 1024), (338, 4096), (70, 2048), (338, 1024), (17, 4096)])
+def test_small_ws_kernel_every_output(dev, orc, m, k):
+    """The grouped small-token kernel with producer and consumer wavefronts (chains seeded with -gsum, int32 sums
+    through two LDS planes, the fold one chunk behind), forced on ragged token counts with 8, 16 and 32 groups
+    (rings of 4 and 8 steps): each epilogue with and without bias, every output bit-exact."""
+    import voxrt_amd as vx
+
+    n_out, g = 256, 128
+    trits, s16, x = _workload(orc, m, k, n_out, g, seed_cfg=11)
+    ws = orc.f16_to_f32(s16)
+    w = vx.TernaryMatrix.from_packed(synth.pack_rows(trits), s16, n_out, k, g)
+    q, xs, _ = orc.quantize(x, g)
+    xa = vx.QuantAct.quantize(_t(x, dev), g)
+    rng = synth.Lcg(61)
+    base = ((rng.take(m * n_out) % 200).astype(np.float32) * np.float32(0.01) - np.float32(1.0)).reshape(m, n_out)
+    bias = (rng.take(n_out) % 100).astype(np.float32) / np.float32(10.0)
+    with vx.kernels.kernel_override(gemm="small", small_ws="on"):
+        for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
+            want = orc.gemm(trits, ws, q, xs, g, y=base.copy(), ep=ep_kind, alpha=alpha)
+            for with_bias in (False, True):
+                y = _t(base, dev)
+                vx.gemm_ep(w, xa, y, _t(bias, dev) if with_bias else None, _ep_of(vx, ep_kind, alpha))
+                exp = (want + bias[None, :]).astype(np.float32) if with_bias else want
+                _assert_bits_equal(y.cpu().numpy(), exp, f"small_ws G=128 {m}x{k}x{n_out} ep={ep_kind} "
+                                                         f"bias={with_bias}")
+
+
+@pytest.mark.parametrize("tile", ["1x8", "2x8"])
+@pytest.mark.parametrize("m,n_out,ep_kind,with_bias", [(338, 4096, 1, False), (70, 384, 0, True), (5, 256, 1, True)])
+def test_small_ws_quantized_output(dev, orc, tile, m, n_out, ep_kind, with_bias):
+    """The producer/consumer kernel writing the next GEMM's activations (one plane, two barriers per chunk): codes,
+    scales and code sums equal the oracle's GEMM -> quantize chain bit for bit, pad tokens zero."""
+    import torch
+
+    import voxrt_amd as vx
+
+    k, g = 1024, 128
+    trits, s16, x = _workload(orc, m, k, n_out, g, seed_cfg=12)
+    ws = orc.f16_to_f32(s16)
+    w = vx.TernaryMatrix.from_packed(synth.pack_rows(trits), s16, n_out, k, g)
+    q, xs, _ = orc.quantize(x, g)
+    xa = vx.QuantAct.quantize(_t(x, dev), g)
+    bias = (synth.Lcg(67).take(n_out) % 100).astype(np.float32) / np.float32(10.0) - np.float32(5.0)
+    want = orc.gemm(trits, ws, q, xs, g, ep=ep_kind)
+    if with_bias:
+        want = (want + bias[None, :]).astype(np.float32)
+    wq, wsc, wgs = orc.quantize(want, 128)
+    with vx.kernels.kernel_override(small_ws="on", small_tile=tile):
+        got = vx.gemm_ep_quantize(w, xa, _t(bias, dev) if with_bias else None, _ep_of(vx, ep_kind, 0.0), 128)
+    torch.cuda.synchronize()
+    tag = f"small_ws {tile} {m}x{k}x{n_out} ep={ep_kind} bias={with_bias}"
+    np.testing.assert_array_equal(got.x.cpu().numpy(), wq, err_msg=f"codes {tag}")
+    st, gt = got.scales_t.cpu().numpy(), got.gsum_t.cpu().numpy()
+    _assert_bits_equal(st[:, :m].T.copy(), wsc, f"scales {tag}")
+    np.testing.assert_array_equal(gt[:, :m].T, wgs, err_msg=f"gsum {tag}")
+    assert not st[:, m:].any() and not gt[:, m:].any(), f"pad tokens not zero {tag}"
+
+
 @pytest.mark.parametrize("m,k,n_out,group,ep_kind,with_bias", [
     (338, 1024, 4096, 128, 1, False),   # the encoder's FFN up-projection at T = 338 (fused epilogue)
     (338, 1024, 4096, 0, 1, True),      # one group (G = K), bias after SiLU

@@ -73,6 +73,7 @@ __device__ __forceinline__ void static_for(F &&f) {
 enum ForcedKernel { kForceNone, kForceDirect, kForceSplitK, kForceLds, kForceBig, kForceSplitG, kForceSmall, kForceStream };
 struct KernelOverrides {
     std::atomic<int> gemm{kForceNone}, tile{0}, small_tile{0}, stream_grid{0};
+    std::atomic<int> small_ws{0};  // grouped small-token kernel with producer/consumer wavefronts: 0 auto, 1 on, 2 off
 };
 KernelOverrides &overrides();
 

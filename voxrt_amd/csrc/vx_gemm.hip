@@ -1360,7 +1360,8 @@ KernelOverrides &overrides() {
 }
 
 // vx_set_kernel_override: name "gemm" (direct, splitk, lds, big, splitg, small, stream), "tile" and "small_tile"
-// ("MTxNT"), "stream_grid" (workgroups, a multiple of 8); NULL or "" clears the name's override.
+// ("MTxNT"), "stream_grid" (workgroups, a multiple of 8), "small_ws" ("on" / "off": the grouped small-token kernel
+// with producer and consumer wavefronts); NULL or "" clears the name's override.
 void set_kernel_override(const char *name, const char *value) {
     require(name != nullptr, "override name must not be NULL");
     const std::string n(name), v(value ? value : "");
@@ -1383,6 +1384,9 @@ void set_kernel_override(const char *name, const char *value) {
         o.tile.store(v.empty() ? 0 : tile_code(v), std::memory_order_relaxed);
     } else if (n == "small_tile") {
         o.small_tile.store(v.empty() ? 0 : tile_code(v), std::memory_order_relaxed);
+    } else if (n == "small_ws") {
+        require(v.empty() || v == "on" || v == "off", "small_ws is \"on\", \"off\" or empty");
+        o.small_ws.store(v.empty() ? 0 : v == "on" ? 1 : 2, std::memory_order_relaxed);
     } else if (n == "stream_grid") {
         const int g = v.empty() ? 0 : atoi(v.c_str());
         require(g == 0 || (g >= 8 && g % 8 == 0), "stream_grid is a positive multiple of 8");

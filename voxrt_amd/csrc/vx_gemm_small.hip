@@ -22,6 +22,10 @@
 // Group-sum output (one group, Store): the exact int32 sums S (the fold's operand) are also stored, to the
 // group_sums buffer [1][n][out], beside y.
 //
+// With 16 or more 128-column groups (FFN-down) a second kernel, tgemm_small_ws_kernel, splits each workgroup into
+// producer wavefronts (the MFMA chains) and consumer wavefronts (the fold, one chunk behind), so the fold of one
+// chunk overlaps the loads and MFMAs of the next.
+//
 // Quantized output (16 x 128 tiles): instead of y, the epilogue writes the next GEMM's activations. The 16 fold
 // threads of a token hold its 128 outputs of one 128-column group after the epilogue and bias, so the group's
 // quantization (QuantAct::quantize_group, packed.rs:527-535: amax, s = amax / 127 or 1, inv = 1 / s, codes
@@ -334,6 +338,245 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
     }
 }
 
+// 128-column groups with producer and consumer wavefronts: eight wavefronts per workgroup, two per SIMD.
+//   * producers (wavefronts 0-3): in chunk c, wavefront p computes group 4c + p over its two 64-column steps (the
+//     same operands, ring and MFMA roles as tgemm_small_kernel), the chain seeded with -gsum of its token and
+//     group so that it ends at S_g exactly, and writes the int32 sums to an LDS plane;
+//   * consumers (wavefronts 4-7): after the barrier that ends chunk c they fold its four groups in ascending order,
+//     acc = fma((float)S_g, xs * ws, acc), while the producers already run chunk c + 1, so on each SIMD the fold's
+//     VALU work overlaps the other wavefront's MFMAs and memory waits; then the epilogue.
+// NPL = 2: chunk c uses plane c % 2, one barrier per chunk (chunk c + 2 overwrites the plane of chunk c only after
+// the barrier that ends chunk c + 1, which each consumer reaches after folding chunk c). NPL = 1 (half the LDS):
+// the producers also wait, before writing chunk c, for a second barrier that the consumers reach after folding
+// chunk c - 1.
+template <int MT, int NT, int D, int EP, bool BIAS, bool QOUT, int MAXG, int NPL>
+__global__ __launch_bounds__(512, NPL == 1 ? 2 : 1) void tgemm_small_ws_kernel(const GemmArgs a, const int n_mt,
+                                                                               const int per_xcd, const int ntiles) {
+    constexpr int BM = 16 * MT, BN = 16 * NT, BNP = BN + 4;
+    constexpr int TPR = BN / 8, RPP = 256 / TPR, R = (BM + RPP - 1) / RPP;
+    static_assert(D % 2 == 0, "a group is two ring steps");
+    static_assert(!QOUT || (BN == 128 && BM % RPP == 0 && EP != VX_EP_ADD_SCALED),
+                  "a quantized output group is one token row of a 128-row tile");
+    __shared__ __attribute__((aligned(16))) int red[NPL][4][BM * BNP];
+    __shared__ __attribute__((aligned(16))) float sxs[MAXG * BM], sws[MAXG * BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = (int)blockIdx.x, tile = (b & 7) * per_xcd + (b >> 3);
+    if (tile >= ntiles) return;  // the whole workgroup: the grid is a multiple of 8
+    const int tm = tile % n_mt, tn = tile / n_mt;
+    const int m0 = (int)a.m_base + tm * BM, n0 = tn * BN;
+    const int inp = (int)a.inp, nk = inp / 64, ng = (int)a.ng, np = (int)a.np, nch = ng / 4;
+
+    if (wave < 4) {
+        // ---- producer: groups 4c + wave, c = 0 .. nch - 1; ring step i is step (i & 1) of group 4 (i >> 1) + wave
+        const int l16 = lane & 15, lq = lane >> 4;
+        const auto xrs = make_rsrc(a.xq, a.xq_bytes);
+        const auto wrs = make_rsrc(a.w, a.w_bytes);
+        const auto grs = make_rsrc(a.xg, a.xs_bytes);
+        uint32_t va[MT], vg[MT];
+#pragma unroll
+        for (int mb = 0; mb < MT; mb++) {
+            va[mb] = (uint32_t)(m0 + 16 * mb + l16) * (uint32_t)inp + 16 * lq;
+            vg[mb] = (uint32_t)(m0 + 16 * mb + l16) * 4;
+        }
+        const int nsteps = 2 * nch;
+        v4i ra[D][MT];
+        uint32_t rb[D][NT], rg[D / 2][MT];
+        auto issue = [&](int i, int slot) __attribute__((always_inline)) {
+            const int g = 4 * (i >> 1) + wave, kb = 2 * g + (i & 1);
+#pragma unroll
+            for (int mb = 0; mb < MT; mb++)
+                ra[slot][mb] = __builtin_amdgcn_raw_buffer_load_b128(xrs, va[mb], kb * 64, 0);
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++)
+                rb[slot][nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)lane * 4, ((n0 / 16 + nb) * nk + kb) * 256, 0);
+            if ((slot & 1) == 0) {
+#pragma unroll
+                for (int mb = 0; mb < MT; mb++)
+                    rg[slot / 2][mb] = __builtin_amdgcn_raw_buffer_load_b32(grs, vg[mb], g * np * 4, 0);
+            }
+        };
+        v4i acc[MT][NT];
+        auto compute = [&](int slot, int i) __attribute__((always_inline)) {
+            v4i bw[NT];
+#pragma unroll
+            for (int nb = 0; nb < NT; nb++) bw[nb] = widen_codes(rb[slot][nb]);
+            if ((slot & 1) == 0) {
+                // the weight operand is the code trit + 1: seeded with -gsum, the chain ends at sum(trit * x)
+#pragma unroll
+                for (int mb = 0; mb < MT; mb++) {
+                    const int s = -(int)rg[slot / 2][mb];
+                    const v4i seed = v4i{s, s, s, s};
+#pragma unroll
+                    for (int nb = 0; nb < NT; nb++)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[nb], ra[slot][mb], seed, 0, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+                    for (int nb = 0; nb < NT; nb++)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[nb], ra[slot][mb], acc[mb][nb], 0, 0, 0);
+                const int c = i >> 1;
+                if (NPL == 1 && c > 0) __syncthreads();  // the consumers have folded chunk c - 1
+                const int buf = NPL == 2 ? (c & 1) : 0;
+#pragma unroll
+                for (int mb = 0; mb < MT; mb++)
+#pragma unroll
+                    for (int nb = 0; nb < NT; nb++)
+                        *(v4i *)&red[buf][wave][(16 * mb + l16) * BNP + 16 * nb + 4 * lq] = acc[mb][nb];
+                __syncthreads();  // chunk c is in its plane
+            }
+        };
+        // the ring in program order (the scheduler would otherwise group the loads by kind and wait for most of
+        // the ring before the first step)
+#pragma unroll
+        for (int i = 0; i < D; i++) {
+            issue(i, i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int s0 = 0; s0 < nsteps - D; s0 += D) {
+#pragma unroll
+            for (int i = 0; i < D; i++) {
+                compute(i, s0 + i);
+                __builtin_amdgcn_sched_barrier(0);
+                issue(s0 + i + D, i);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < D; i++) {
+            compute(i, nsteps - D + i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return;
+    }
+
+    // ---- consumer: thread ct owns token rows tt0 + r * RPP of the tile and output rows c0 .. c0 + 7
+    const int ct = tid - 256;
+    const int tt0 = ct / TPR, c0 = (ct % TPR) * 8, o0 = n0 + c0;
+    const uint32_t out4 = (uint32_t)a.out * 4;
+    const auto srs = make_rsrc(a.xs, a.xs_bytes);
+    const auto wsrs = make_rsrc(a.ws_t, a.ws_bytes);
+    const auto yrs = make_rsrc(a.y, a.y_bytes);
+    const auto brs = make_rsrc(a.bias, BIAS ? (uint32_t)(a.out * 4) : 0u);
+    // the token and weight scales of every group of the tile (entries past the last group read zeros, unused)
+#pragma unroll
+    for (int q = 0; q < (MAXG * BM + 255) / 256; q++) {
+        const int i = ct + 256 * q, g = i / BM, k = i % BM;
+        if (i < MAXG * BM)
+            sxs[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                srs, g < ng ? (uint32_t)(g * np + m0 + k) * 4 : kOff, 0, 0));
+    }
+#pragma unroll
+    for (int q = 0; q < (MAXG * BN + 255) / 256; q++) {
+        const int i = ct + 256 * q, g = i / BN, k = i % BN;
+        if (i < MAXG * BN)
+            sws[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                wsrs, g < ng ? (uint32_t)(g * (int)a.out_pad + n0 + k) * 4 : kOff, 0, 0));
+    }
+    v4i blo = v4i{0, 0, 0, 0}, bhi = v4i{0, 0, 0, 0};
+    if constexpr (BIAS) {
+        blo = __builtin_amdgcn_raw_buffer_load_b128(brs, (uint32_t)o0 * 4, 0, 0);
+        bhi = __builtin_amdgcn_raw_buffer_load_b128(brs, (uint32_t)o0 * 4 + 16, 0, 0);
+    }
+    v4i olo[EP == VX_EP_ADD_SCALED ? R : 1], ohi[EP == VX_EP_ADD_SCALED ? R : 1];
+    if constexpr (EP == VX_EP_ADD_SCALED) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t so = (uint32_t)(m0 + tt0 + r * RPP) * out4 + (uint32_t)o0 * 4;
+            olo[r] = __builtin_amdgcn_raw_buffer_load_b128(yrs, so, 0, 0);
+            ohi[r] = __builtin_amdgcn_raw_buffer_load_b128(yrs, so + 16, 0, 0);
+        }
+    }
+    float accf[R][8];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) accf[r][j] = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        if (NPL == 1 && c > 0) __syncthreads();  // chunk c - 1 folded: the producers may overwrite the plane
+        __syncthreads();                          // chunk c is in its plane (the first one also orders the tables)
+        const int buf = NPL == 2 ? (c & 1) : 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const int g = 4 * c + w;
+            const float4 wa = *(const float4 *)&sws[g * BN + c0];
+            const float4 wb = *(const float4 *)&sws[g * BN + c0 + 4];
+            const float wsv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int tt = tt0 + r * RPP;
+                if (BM % RPP != 0 && tt >= BM) continue;
+                const float xs = sxs[g * BM + tt];
+                const v4i lo = *(const v4i *)&red[buf][w][tt * BNP + c0];
+                const v4i hi = *(const v4i *)&red[buf][w][tt * BNP + c0 + 4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    accf[r][j] = __builtin_fmaf((float)lo[j], xs * wsv[j], accf[r][j]);
+                    accf[r][4 + j] = __builtin_fmaf((float)hi[j], xs * wsv[4 + j], accf[r][4 + j]);
+                }
+            }
+        }
+    }
+
+    // epilogue (kernels/mod.rs:41-48), bias after it; tokens outside [t0, t1) are not written
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int t = m0 + tt0 + r * RPP;
+        v4i lo, hi;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float v = accf[r][j];
+            float res = v;
+            if constexpr (EP == VX_EP_SILU) res = silu_fast(v);
+            if constexpr (EP == VX_EP_ADD_SCALED)
+                res = __builtin_fmaf(a.alpha, v, __int_as_float(j < 4 ? olo[r][j] : ohi[r][j - 4]));
+            if constexpr (BIAS) res = res + __int_as_float(j < 4 ? blo[j] : bhi[j - 4]);
+            if (j < 4)
+                lo[j] = __float_as_int(res);
+            else
+                hi[j - 4] = __float_as_int(res);
+        }
+        if constexpr (QOUT) {
+            // quantize_group over the token's 128 outputs: 8 per lane on 16 adjacent lanes
+            float m = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(__int_as_float(lo[j])), fabsf(__int_as_float(hi[j]))));
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            const float s = m == 0.0f ? 1.0f : m / 127.0f;
+            const float inv = 1.0f / s;
+            uint32_t w0 = 0, w1 = 0;
+            int sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int8_t q0 = code_of(__int_as_float(lo[j]), inv), q1 = code_of(__int_as_float(hi[j]), inv);
+                sum += (int)q0 + (int)q1;
+                w0 |= (uint32_t)(uint8_t)q0 << (8 * j);
+                w1 |= (uint32_t)(uint8_t)q1 << (8 * j);
+            }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            const int64_t gi = (int64_t)(o0 / 128) * a.np + t;
+            if (t < a.n) {
+                *(uint2 *)(a.qo + (int64_t)t * a.out + o0) = make_uint2(w0, w1);
+                if ((ct & 15) == 0) {
+                    a.qs[gi] = s;
+                    a.qg[gi] = sum;
+                }
+            } else if (t < a.np && (ct & 15) == 0) {  // pad tokens: zero scale and code sum
+                a.qs[gi] = 0.0f;
+                a.qg[gi] = 0;
+            }
+        } else if (t >= a.t0 && t < a.t1 && (BM % RPP == 0 || tt0 + r * RPP < BM)) {
+            const uint32_t so = (uint32_t)t * out4 + (uint32_t)o0 * 4;
+            __builtin_amdgcn_raw_buffer_store_b128(lo, yrs, so, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(hi, yrs, so + 16, 0, 0);
+        }
+    }
+}
+
 // deepest ring of K steps whose operands (MT activation and NT weight registers per step) fit in 128 registers
 constexpr int max_ring(int mt, int nt) { return 128 / (4 * mt + nt) >= 8 ? 8 : 128 / (4 * mt + nt) >= 4 ? 4 : 2; }
 
@@ -440,6 +683,56 @@ void launch_small(const GemmArgs &a, const SmallPlan &p, int grid, int n_mt, int
 #undef VX_TILE
 }
 
+template <int MT, int NT, int NPL, int D, int MAXG>
+void launch_ws_g(const GemmArgs &a, int grid, int n_mt, int per_xcd, int ntiles, hipStream_t st) {
+    const bool bias = a.bias != nullptr;
+    if constexpr (NT == 8) {  // 128-row tiles: the quantized output
+#define VX_WSQ(EP)                                                                                                \
+    (bias ? tgemm_small_ws_kernel<MT, NT, D, EP, true, true, MAXG, NPL>                                           \
+          : tgemm_small_ws_kernel<MT, NT, D, EP, false, true, MAXG, NPL>)
+        auto k = a.ep == VX_EP_SILU ? VX_WSQ(VX_EP_SILU) : VX_WSQ(VX_EP_STORE);
+#undef VX_WSQ
+        k<<<grid, 512, 0, st>>>(a, n_mt, per_xcd, ntiles);
+    } else {
+#define VX_WS(EP)                                                                                                 \
+    (bias ? tgemm_small_ws_kernel<MT, NT, D, EP, true, false, MAXG, NPL>                                          \
+          : tgemm_small_ws_kernel<MT, NT, D, EP, false, false, MAXG, NPL>)
+        auto k = a.ep == VX_EP_SILU ? VX_WS(VX_EP_SILU) : a.ep == VX_EP_ADD_SCALED ? VX_WS(VX_EP_ADD_SCALED)
+                                                                                   : VX_WS(VX_EP_STORE);
+#undef VX_WS
+        k<<<grid, 512, 0, st>>>(a, n_mt, per_xcd, ntiles);
+    }
+}
+
+// The producer/consumer kernel for 8 groups (K = 1024, a ring of 4 steps per producer) or 16 / 32 groups (a ring
+// of 8): 32 x 64 tiles with two LDS planes for y, 16 x 128 or 32 x 128 tiles with one plane for the quantized
+// output (the next GEMM's activations, 8 groups only). Launches nothing and returns false for other shapes or a
+// forced tile it is not built for.
+bool launch_ws(const GemmArgs &a, bool qout, int fm, int fn, hipStream_t st) {
+    if (a.ng != 8 && a.ng != 16 && a.ng != 32) return false;
+    int mt = qout ? 1 : 2, nt = qout ? 8 : 4;
+    if (fm) {
+        if (qout ? !((fm == 1 || fm == 2) && fn == 8) : !(fm == 2 && fn == 4)) return false;
+        mt = fm;
+        nt = fn;
+    }
+    if (a.out % (16 * nt) != 0 || (qout && a.ng != 8)) return false;
+    const int64_t ntok = a.t1 - a.m_base;
+    const int n_mt = (int)((ntok + 16 * mt - 1) / (16 * mt)), tiles = n_mt * (int)(a.out / (16 * nt));
+    const int per_xcd = (tiles + 7) / 8, grid = 8 * per_xcd;
+    if (qout) {
+        if (mt == 1)
+            launch_ws_g<1, 8, 1, 4, 8>(a, grid, n_mt, per_xcd, tiles, st);
+        else
+            launch_ws_g<2, 8, 1, 4, 8>(a, grid, n_mt, per_xcd, tiles, st);
+    } else if (a.ng == 8) {
+        launch_ws_g<2, 4, 2, 4, 8>(a, grid, n_mt, per_xcd, tiles, st);
+    } else {
+        launch_ws_g<2, 4, 2, 8, kMaxG>(a, grid, n_mt, per_xcd, tiles, st);
+    }
+    return true;
+}
+
 }  // namespace
 
 bool gemm_small(const GemmArgs &a, hipStream_t st) {
@@ -457,6 +750,13 @@ bool gemm_small(const GemmArgs &a, hipStream_t st) {
         while (p.d * 2 <= max_ring(1, 8) && steps % (p.d * 2) == 0) p.d *= 2;
         if (grouped && p.d < 2) return false;
         const int n_mt = (int)((a.n + 15) / 16), per_xcd = (p.tiles + 7) / 8;
+        if (grouped && overrides().small_ws.load(std::memory_order_relaxed) == 1) {
+            const int ft = overrides().small_tile.load(std::memory_order_relaxed);
+            if (launch_ws(a, true, ft >> 4, ft & 15, st)) {
+                hip_check(hipGetLastError(), "tgemm_small_ws launch");
+                return true;
+            }
+        }
         if (grouped)
             launch_small<true>(a, p, 8 * per_xcd, n_mt, per_xcd, p.tiles, st);
         else
@@ -477,6 +777,14 @@ bool gemm_small(const GemmArgs &a, hipStream_t st) {
     const int fm = ft >> 4, fn = ft & 15;
     // up to 1024 tokens; longer token ranges go to the kernels built for throughput
     if (a.t1 - a.m_base > 1024 && forced != kForceSmall) return false;
+    // the producer/consumer kernel by default for 16 or more groups (K >= 2048: FFN-down), where the fold of many
+    // chunks overlaps the next chunk's loads and MFMAs (T = 125 / 338 / 750: 11.1 / 11.5 / 18.6 -> 9.2 / 9.3 / 16.9
+    // us); with 8 groups the four-wavefront kernel is as fast or faster
+    const int ws = overrides().small_ws.load(std::memory_order_relaxed);
+    if (grouped && (ws == 1 || (ws == 0 && a.ng >= 16 && !(fm && fn))) && launch_ws(a, false, fm, fn, st)) {
+        hip_check(hipGetLastError(), "tgemm_small_ws launch");
+        return true;
+    }
     const SmallPlan p = plan_small(a, grouped, fm, fn);
     if (p.mt == 0) return false;
     const int64_t ntok = a.t1 - a.m_base;
