@@ -110,6 +110,26 @@ def test_linear_f32_equals_oracle(dev, orc, n, in_f, out_f, relu):
     _bits_equal(got, want, f"linear {n}x{in_f}x{out_f}")
 
 
+@pytest.mark.parametrize("kernel", ["lds", "mfma1x1", "mfma2x1", "mfma2x2"])
+@pytest.mark.parametrize("n,in_f,out_f,relu", [(6, 256, 40, True), (700, 256, 256, True), (94, 4096, 1024, False),
+                                               (33, 4100, 70, False), (338, 4096, 1024, False), (5, 4, 3, False),
+                                               (77, 302, 19, True)])
+def test_linear_f32_each_kernel(dev, orc, kernel, n, in_f, out_f, relu):
+    """Both f32 linear kernels, forced: the LDS-broadcast one and the matrix-core one (K = 1 MFMA per 4-column step,
+    one block per running sum) with each tile (partial output tiles, partial 128-column slabs, a partial last quad
+    of steps, a tail, the subsampling's final linear), bit-exact."""
+    import voxrt_amd as vx
+    from voxrt_amd import encoder as E
+
+    x, w, b = _x(19, n, in_f), _x(20, out_f, in_f, scale=0.05), _x(21, out_f)
+    want = orc.linear_f32(x, w, b)
+    if relu:
+        want = np.where(want > 0, want, np.float32(0)).astype(np.float32)
+    with vx.kernels.kernel_override(linear=kernel):
+        got = E.linear_f32(_t(x, dev), _t(w, dev), _t(b, dev), relu=relu).cpu().numpy()
+    _bits_equal(got, want, f"linear kernel={kernel} {n}x{in_f}x{out_f}")
+
+
 @pytest.mark.parametrize("t,n_mels,c,d", [(41, 40, 16, 96), (2704, 128, 256, 1024)])
 def test_subsampling_equals_oracle(dev, orc, t, n_mels, c, d):
     from voxrt_amd import encoder as E

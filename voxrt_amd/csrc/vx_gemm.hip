@@ -1361,7 +1361,8 @@ KernelOverrides &overrides() {
 
 // vx_set_kernel_override: name "gemm" (direct, splitk, lds, big, splitg, small, stream), "tile" and "small_tile"
 // ("MTxNT"), "stream_grid" (workgroups, a multiple of 8), "small_ws" ("on" / "off": the grouped small-token kernel
-// with producer and consumer wavefronts); NULL or "" clears the name's override.
+// with producer and consumer wavefronts), "linear" (the f32 linear: "lds", or the
+// matrix-core kernel's tile, "mfma1x1" / "mfma2x1" / "mfma2x2"); NULL or "" clears the name's override.
 void set_kernel_override(const char *name, const char *value) {
     require(name != nullptr, "override name must not be NULL");
     const std::string n(name), v(value ? value : "");
@@ -1387,6 +1388,11 @@ void set_kernel_override(const char *name, const char *value) {
     } else if (n == "small_ws") {
         require(v.empty() || v == "on" || v == "off", "small_ws is \"on\", \"off\" or empty");
         o.small_ws.store(v.empty() ? 0 : v == "on" ? 1 : 2, std::memory_order_relaxed);
+    } else if (n == "linear") {
+        const int k = v.empty() ? 0 : v == "lds" ? -1 : v == "mfma1x1" ? 111 : v == "mfma2x1" ? 121
+                                                        : v == "mfma2x2" ? 122 : -2;
+        require(k != -2, "linear is \"lds\", \"mfma1x1\", \"mfma2x1\", \"mfma2x2\" or empty");
+        o.linear.store(k, std::memory_order_relaxed);
     } else if (n == "stream_grid") {
         const int g = v.empty() ? 0 : atoi(v.c_str());
         require(g == 0 || (g >= 8 && g % 8 == 0), "stream_grid is a positive multiple of 8");

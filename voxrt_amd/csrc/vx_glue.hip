@@ -12,7 +12,7 @@
 #include <cmath>
 #include <vector>
 
-#include "vx_internal.h"
+#include "vx_gemm.h"
 
 namespace vx {
 
@@ -210,6 +210,140 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict
     }
 }
 
+// The same sums on the fp32 matrix cores. v_mfma_f32_16x16x1f32 computes four independent 16 x 16 blocks of
+// D = A (x) B + C with K = 1, each element one fused multiply-add with a single rounding; it equals fmaf bit for bit
+// (checked on the device against fmaf over random and special operands: denormals, infinities, NaN, exact
+// cancellation, signed zeros). Block c of one instruction is running sum c of the reference's lanes, so one
+// instruction is one 4-column step for 16 tokens x 16 outputs:
+//   lane l supplies A = x[token l % 16][4s + l / 16] and B = w[output l % 16][4s + l / 16];
+//   D register r of lane l is running sum r / 4 of token 4 * (l / 16) + r % 4 and output l % 16.
+// The slabs of x and w are staged in LDS de-interleaved by running sum, [c][row][step] with a row pitch of 36
+// floats (16 consecutive rows of one c start in distinct bank quads), so one 16-byte read gives a lane four steps.
+// Only the steps below in_f / 4 are issued (padding is never accumulated: fma(0, 0, -0) would be +0); the
+// unfused tail and (hsum4 + tail) + bias follow in the epilogue. A workgroup of four wavefronts (2 x 2) owns
+// (32 WT) tokens x (32 WO) outputs, a wavefront WT x WO blocks of 16 x 16.
+constexpr int kLinMK = 128;  // slab columns (32 steps)
+
+template <bool RELU, int WT, int WO>
+__global__ __launch_bounds__(256) void linear_f32_mfma_kernel(const float *__restrict__ x, int n, int in_f,
+                                                             const float *__restrict__ w,
+                                                             const float *__restrict__ b, int out_f,
+                                                             float *__restrict__ y) {
+    constexpr int BM = 32 * WT, BN = 32 * WO, KS = kLinMK, SP = KS / 4 + 4;  // SP: row pitch (floats)
+    constexpr int QX = BM * KS / 16 / 256, QW = BN * KS / 16 / 256;           // 16-column pieces per thread
+    static_assert(QX >= 1 && QW >= 1, "a thread stages at least one piece of each operand");
+    __shared__ __attribute__((aligned(16))) float sx[4][BM][SP], sw[4][BN][SP];
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.y * BM, o0 = blockIdx.x * BN;
+    const int l16 = lane & 15, lc = lane >> 4;                           // row in a block, running sum
+    const int wt0 = (wv & 1) * 16 * WT, wo0 = (wv >> 1) * 16 * WO;       // the wavefront's blocks in the tile
+    const int c4 = in_f / 4 * 4, nsteps = c4 / 4, nslab = (c4 + KS - 1) / KS;
+    typedef float v16f __attribute__((ext_vector_type(16)));
+    v16f acc[WT][WO];
+#pragma unroll
+    for (int i = 0; i < WT; i++)
+#pragma unroll
+        for (int j = 0; j < WO; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    // staging: piece p of an operand is row p / (KS / 16), columns 16 (p % (KS / 16)) .. + 15 of the slab, loaded as
+    // four quads and written as four quads of consecutive steps, one per running sum
+    float4 px[QX][4], pq[QW][4];
+    auto fetch = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < QX; q++) {
+            const int p = tid + 256 * q, r = p / (KS / 16), c = k0 + 16 * (p % (KS / 16));
+            const float *src = x + (int64_t)min(t0 + r, n - 1) * in_f + c;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                px[q][j] = c + 4 * j < c4 ? *(const float4 *)(src + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int q = 0; q < QW; q++) {
+            const int p = tid + 256 * q, r = p / (KS / 16), c = k0 + 16 * (p % (KS / 16));
+            const float *src = w + (int64_t)min(o0 + r, out_f - 1) * in_f + c;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                pq[q][j] = c + 4 * j < c4 ? *(const float4 *)(src + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    auto stash = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < QX; q++) {
+            const int p = tid + 256 * q, r = p / (KS / 16), s = 4 * (p % (KS / 16));
+            *(float4 *)&sx[0][r][s] = make_float4(px[q][0].x, px[q][1].x, px[q][2].x, px[q][3].x);
+            *(float4 *)&sx[1][r][s] = make_float4(px[q][0].y, px[q][1].y, px[q][2].y, px[q][3].y);
+            *(float4 *)&sx[2][r][s] = make_float4(px[q][0].z, px[q][1].z, px[q][2].z, px[q][3].z);
+            *(float4 *)&sx[3][r][s] = make_float4(px[q][0].w, px[q][1].w, px[q][2].w, px[q][3].w);
+        }
+#pragma unroll
+        for (int q = 0; q < QW; q++) {
+            const int p = tid + 256 * q, r = p / (KS / 16), s = 4 * (p % (KS / 16));
+            *(float4 *)&sw[0][r][s] = make_float4(pq[q][0].x, pq[q][1].x, pq[q][2].x, pq[q][3].x);
+            *(float4 *)&sw[1][r][s] = make_float4(pq[q][0].y, pq[q][1].y, pq[q][2].y, pq[q][3].y);
+            *(float4 *)&sw[2][r][s] = make_float4(pq[q][0].z, pq[q][1].z, pq[q][2].z, pq[q][3].z);
+            *(float4 *)&sw[3][r][s] = make_float4(pq[q][0].w, pq[q][1].w, pq[q][2].w, pq[q][3].w);
+        }
+    };
+    fetch(0);
+    for (int sl = 0; sl < nslab; sl++) {
+        if (sl > 0) __syncthreads();  // every wavefront is done with the previous slab
+        stash();
+        __syncthreads();
+        if (sl + 1 < nslab) fetch((sl + 1) * KS);
+        const int sn = min(KS / 4, nsteps - sl * (KS / 4));  // steps in this slab
+        auto quad = [&](int s4) __attribute__((always_inline)) {  // steps s4 .. s4 + 3
+            float4 xa[WT], wa[WO];
+#pragma unroll
+            for (int i = 0; i < WT; i++) xa[i] = *(const float4 *)&sx[lc][wt0 + 16 * i + l16][s4];
+#pragma unroll
+            for (int j = 0; j < WO; j++) wa[j] = *(const float4 *)&sw[lc][wo0 + 16 * j + l16][s4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int i = 0; i < WT; i++)
+#pragma unroll
+                    for (int j = 0; j < WO; j++) {
+                        const float av = e == 0 ? xa[i].x : e == 1 ? xa[i].y : e == 2 ? xa[i].z : xa[i].w;
+                        const float bv = e == 0 ? wa[j].x : e == 1 ? wa[j].y : e == 2 ? wa[j].z : wa[j].w;
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x1f32(av, bv, acc[i][j], 0, 0, 0);
+                    }
+        };
+        auto single = [&](int s) __attribute__((always_inline)) {  // one step (a slab's last partial quad)
+#pragma unroll
+            for (int i = 0; i < WT; i++)
+#pragma unroll
+                for (int j = 0; j < WO; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x1f32(sx[lc][wt0 + 16 * i + l16][s],
+                                                                    sw[lc][wo0 + 16 * j + l16][s], acc[i][j], 0, 0, 0);
+        };
+        int s = 0;
+#pragma unroll 2
+        for (; s + 4 <= sn; s += 4) quad(s);
+        for (; s < sn; s++) single(s);
+    }
+    // epilogue: lane l holds, for output o0 + wo0 + 16 j + l % 16, tokens t0 + wt0 + 16 i + 4 (l / 16) + e
+#pragma unroll
+    for (int j = 0; j < WO; j++) {
+        const int o = o0 + wo0 + 16 * j + l16;
+        if (o >= out_f) continue;
+        const float bo = b ? b[o] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < WT; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int t = t0 + wt0 + 16 * i + 4 * lc + e;
+                if (t >= n) continue;
+                float tail = 0.0f;
+                for (int col = c4; col < in_f; col++) tail += w[(int64_t)o * in_f + col] * x[(int64_t)t * in_f + col];
+                float v = ((acc[i][j][e] + acc[i][j][4 + e]) + (acc[i][j][8 + e] + acc[i][j][12 + e])) + tail;
+                v = v + bo;
+                if (RELU) v = v > 0.0f ? v : 0.0f;
+                y[(int64_t)t * out_f + o] = v;
+            }
+    }
+}
+
 // One token: gemv_portable (tensor.rs:284-303): rows below out_f/4*4 by dot_lanes8 (fused lanes over 8-column
 // steps, lane-wise a + b, hsum4, tail unfused), the others by dot (8 unfused lane sums summed in order, tail).
 template <bool RELU>
@@ -255,9 +389,31 @@ void linear_f32(const float *x, int64_t n, int64_t in_f, const float *w, const f
         auto k = relu ? gemv_f32_kernel<true> : gemv_f32_kernel<false>;
         k<<<(unsigned)((out_f + 255) / 256), 256, 0, st>>>(x, (int)in_f, w, b, (int)out_f, y);
     } else {
-        auto k = relu ? linear_f32_kernel<true> : linear_f32_kernel<false>;
-        k<<<dim3((unsigned)((out_f + LO - 1) / LO), (unsigned)((n + LTT - 1) / LTT)), 256, 0, st>>>(
-            x, (int)n, (int)in_f, w, b, (int)out_f, y);
+        // the matrix-core kernel where its 16-byte loads are aligned: 64 x 64 tiles when they give 256 workgroups
+        // (the subsampling's pointwise convolutions), else 32 x 32 (its final linear); else the LDS-broadcast kernel
+        const bool aligned = in_f % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                             reinterpret_cast<uintptr_t>(w) % 16 == 0;
+        int kind = overrides().linear.load(std::memory_order_relaxed);
+        auto wgs = [&](int bm, int bn) { return ((n + bm - 1) / bm) * ((out_f + bn - 1) / bn); };
+        if (kind == 0) kind = wgs(64, 64) >= 256 ? 122 : 111;
+        if (aligned && kind > 0) {
+            const int wt = kind / 10 % 10, wo = kind % 10;
+            const dim3 grid((unsigned)((out_f + 32 * wo - 1) / (32 * wo)), (unsigned)((n + 32 * wt - 1) / (32 * wt)));
+#define VX_LINM(WT, WO)                                                                                           \
+    (relu ? linear_f32_mfma_kernel<true, WT, WO> : linear_f32_mfma_kernel<false, WT, WO>)<<<grid, 256, 0, st>>>(   \
+        x, (int)n, (int)in_f, w, b, (int)out_f, y)
+            if (wt == 2 && wo == 2)
+                VX_LINM(2, 2);
+            else if (wt == 2)
+                VX_LINM(2, 1);
+            else
+                VX_LINM(1, 1);
+#undef VX_LINM
+        } else {
+            auto k = relu ? linear_f32_kernel<true> : linear_f32_kernel<false>;
+            k<<<dim3((unsigned)((out_f + LO - 1) / LO), (unsigned)((n + LTT - 1) / LTT)), 256, 0, st>>>(
+                x, (int)n, (int)in_f, w, b, (int)out_f, y);
+        }
     }
     hip_check(hipGetLastError(), "linear_f32 kernel launch");
 }
