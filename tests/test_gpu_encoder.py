@@ -130,6 +130,39 @@ def test_linear_f32_each_kernel(dev, orc, kernel, n, in_f, out_f, relu):
     _bits_equal(got, want, f"linear kernel={kernel} {n}x{in_f}x{out_f}")
 
 
+@pytest.mark.parametrize("kernel", ["mfma1x1", "mfma2x2"])
+def test_linear_f32_matrix_cores_on_special_operands(dev, orc, kernel):
+    """The matrix-core f32 linear relies on the K = 1 MFMA rounding like fmaf (one rounding, denormals kept, signed
+    zeros and exact cancellation as IEEE): operands made of denormals, zeros of both signs, values that cancel
+    exactly, huge and tiny magnitudes, infinities and NaN, against the oracle's fmaf chains, bit for bit."""
+    import voxrt_amd as vx
+    from voxrt_amd import encoder as E
+
+    rng = np.random.default_rng(23)
+    n, in_f, out_f = 70, 512, 96
+    bits = rng.integers(0, 2**32, size=(n + out_f) * in_f, dtype=np.uint64).astype(np.uint32)
+    kind = rng.integers(0, 6, size=bits.size)
+    mant_sign = bits & np.uint32(0x807FFFFF)
+    exps = np.where(kind == 0, 0,                                   # denormals and signed zeros
+           np.where(kind == 1, 1 + (bits >> 24) % 8,                # tiny normals
+           np.where(kind == 2, 120 + (bits >> 24) % 16,             # ordinary
+           np.where(kind == 3, 230 + (bits >> 24) % 24, 127))))     # huge / ones
+    vals = (mant_sign | (exps.astype(np.uint32) << 23)).view(np.float32)
+    vals[kind == 5] = np.where(bits[kind == 5] & 1, np.float32(-0.0), np.float32(0.0))
+    x = vals[:n * in_f].reshape(n, in_f).copy()
+    w = vals[n * in_f:].reshape(out_f, in_f).copy()
+    x[3, :] = -x[4, :]                                              # exact cancellation between rows
+    x[5, 7], w[9, 11] = np.inf, np.nan
+    b = rng.standard_normal(out_f).astype(np.float32)
+    b[::5] = -0.0
+    want = orc.linear_f32(x, w, b)
+    with vx.kernels.kernel_override(linear=kernel):
+        got = E.linear_f32(_t(x, dev), _t(w, dev), _t(b, dev)).cpu().numpy()
+    g, wv = got.view(np.uint32), want.view(np.uint32)
+    same = (g == wv) | (np.isnan(got) & np.isnan(want))
+    assert same.all(), f"{(~same).sum()} differ, first {np.argwhere(~same)[0]}"
+
+
 @pytest.mark.parametrize("t,n_mels,c,d", [(41, 40, 16, 96), (2704, 128, 256, 1024)])
 def test_subsampling_equals_oracle(dev, orc, t, n_mels, c, d):
     from voxrt_amd import encoder as E

@@ -151,12 +151,15 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const float *__restrict_
         attn_vt_item(((int)blockIdx.x - rows_blocks) * 4 + wv, qkv, D, W);
 }
 
-// LDS plan of attn_core_kernel (bytes): s1 [16][s1w] f32, s2 [16][s2w] f32, pq [16][tv] int8, row stats.
+// LDS plan of attn_core_kernel (bytes): s1 [16][s1w] f32, s2 [16][s2w] f32, pq [16][tv] int8, row stats (kRowv
+// words: [0,16) max, [16,32) 1/sum, [32,48) probability scale, [64,192) and [192,320) the quantized output's
+// per-wavefront row maxima and code sums).
+constexpr int kCoreWaves = 8, kRowv = 320;
 __host__ __device__ inline int s1w_of(int t) { return up16(t) + 4; }
 // the band of a block spans at most t + 45 positions after its start is rounded down to a 16-block
 __host__ __device__ inline int s2w_of(int t) { return up16(t + 48) + 4; }
 __host__ __device__ inline size_t core_lds_bytes(int t) {
-    return (size_t)16 * s1w_of(t) * 4 + (size_t)16 * s2w_of(t) * 4 + (size_t)16 * up64(t) + 192 * 4;
+    return (size_t)16 * s1w_of(t) * 4 + (size_t)16 * s2w_of(t) * 4 + (size_t)16 * up64(t) + kRowv * 4;
 }
 
 // ctx written as the o-projection's int8 activations (Attention::forward_fused, encoder.rs:180-183: attn_core_int8
@@ -169,15 +172,17 @@ struct AttnQOut {
     int np;        // npad(nseg * t)
 };
 
+// Eight wavefronts: the key and band blocks are dealt out over them, each query row's softmax runs on 32 lanes, and
+// each wavefront owns one 16-channel block of the context.
 template <bool QOUT>
-__global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, float scaling, float *__restrict__ ctx,
-                                                        AttnQOut Q) {
+__global__ __launch_bounds__(64 * kCoreWaves) void attn_core_kernel(AttnDims D, AttnWs W, float scaling,
+                                                                    float *__restrict__ ctx, AttnQOut Q) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int s1w = s1w_of(D.t), s2w = s2w_of(D.t);
     float *s1 = (float *)smem;
     float *s2 = s1 + 16 * s1w;
     int8_t *pq = (int8_t *)(s2 + 16 * s2w);
-    float *rowv = (float *)(pq + 16 * D.tv);  // [0,16) max, [16,32) 1/sum, [32,48) prob scale, [64,192) QOUT
+    float *rowv = (float *)(pq + 16 * D.tv);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.y, i0 = blockIdx.x * 16;
     const int t = D.t;
@@ -215,15 +220,15 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
         qus[e] = W.qus[h * D.tp + i0 + drow + e];
         qvs[e] = W.qvs[h * D.tp + i0 + drow + e];
     }
-    // content scores: key block kb -> s1[row][16*kb + col]. A wave takes blocks wave, wave+4, ...; the loads of
+    // content scores: key block kb -> s1[row][16*kb + col]. A wave takes blocks wave, wave+8, ...; the loads of
     // kPF of its blocks are issued before their MFMAs (past the last block: a repeat of it, not used)
-    constexpr int kPF = 4;
-    for (int kb0 = wave; kb0 < nkb; kb0 += 4 * kPF) {
+    constexpr int kPF = 4, NW = kCoreWaves;
+    for (int kb0 = wave; kb0 < nkb; kb0 += NW * kPF) {
         v4i b0[kPF], b1[kPF];
         float ksv[kPF];
 #pragma unroll
         for (int p = 0; p < kPF; p++) {
-            const int kb = min(kb0 + 4 * p, nkb - 1);
+            const int kb = min(kb0 + NW * p, nkb - 1);
             const int8_t *kr = W.kq + ((int64_t)h * D.tp + kb * 16 + arow) * kDh + 16 * aq;
             b0[p] = *(const v4i *)kr;
             b1[p] = *(const v4i *)(kr + 64);
@@ -231,7 +236,7 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
         }
 #pragma unroll
         for (int p = 0; p < kPF; p++) {
-            const int kb = kb0 + 4 * p;
+            const int kb = kb0 + NW * p;
             if (kb < nkb) {
                 v4i acc = {0, 0, 0, 0};
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au0, b0[p], acc, 0, 0, 0);
@@ -243,12 +248,12 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
         }
     }
     // position band: block pb -> s2[row][16*pb' + col], position pb0 + 16*pb' + col (loads ahead as above)
-    for (int q0 = wave; q0 < npb; q0 += 4 * kPF) {
+    for (int q0 = wave; q0 < npb; q0 += NW * kPF) {
         v4i b0[kPF], b1[kPF];
         float rsv[kPF];
 #pragma unroll
         for (int p = 0; p < kPF; p++) {
-            const int p0 = pb0 + min(q0 + 4 * p, npb - 1) * 16;
+            const int p0 = pb0 + min(q0 + NW * p, npb - 1) * 16;
             const int8_t *rr = W.rq + ((int64_t)h * D.rp + p0 + arow) * kDh + 16 * aq;
             b0[p] = *(const v4i *)rr;
             b1[p] = *(const v4i *)(rr + 64);
@@ -256,7 +261,7 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
         }
 #pragma unroll
         for (int p = 0; p < kPF; p++) {
-            const int pb = q0 + 4 * p;
+            const int pb = q0 + NW * p;
             if (pb < npb) {
                 v4i acc = {0, 0, 0, 0};
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0[p], acc, 0, 0, 0);
@@ -269,23 +274,23 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
     }
     __syncthreads();
     const int nrows = imax - i0 + 1;  // valid query rows of the block
-    // per row (16 lanes, wave w rows 4w .. 4w+3): score = S1 + S2[t-1-i+j] in place in s1, the row max of
+    // per row (32 lanes, wave w rows 2w, 2w+1): score = S1 + S2[t-1-i+j] in place in s1, the row max of
     // score * scaling, then exp_poly(score * scaling - max) in place
     {
-        const int r = wave * 4 + (lane >> 4), l16 = lane & 15;
+        const int r = wave * 2 + (lane >> 5), l32 = lane & 31;
         float m = -INFINITY;
         if (r < nrows) {
             const float *s2r = s2 + r * s2w + (t - 1 - (i0 + r) - pb0);
-            for (int j = l16; j < t; j += 16) {
+            for (int j = l32; j < t; j += 32) {
                 const float sc = s1[r * s1w + j] + s2r[j];
                 s1[r * s1w + j] = sc;
                 m = fmaxf(m, sc * scaling);
             }
         }
 #pragma unroll
-        for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
         if (r < nrows)
-            for (int j = l16; j < t; j += 16) s1[r * s1w + j] = exp_poly(s1[r * s1w + j] * scaling - m);
+            for (int j = l32; j < t; j += 32) s1[r * s1w + j] = exp_poly(s1[r * s1w + j] * scaling - m);
     }
     __syncthreads();
     // row sums in the reference's order: lane 4r + l keeps the running sum of columns j = 4q + l
@@ -305,69 +310,60 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
             for (int j = t4; j < t; j++) sum += s1[r * s1w + j];
         if (l == 0) rowv[16 + r] = 1.0f / sum;
     }
-    // probability quantization: amax per row (16 lanes per row), codes into pq, zero to tv
+    // probability quantization: amax per row (32 lanes per row), codes into pq, zero to tv
     {
-        const int r = wave * 4 + (lane >> 4), l16 = lane & 15;
+        const int r = wave * 2 + (lane >> 5), l32 = lane & 31;
         float m = 0.0f;
         if (r < nrows)
-            for (int j = l16; j < t; j += 16) m = fmaxf(m, fabsf(s1[r * s1w + j]));
+            for (int j = l32; j < t; j += 32) m = fmaxf(m, fabsf(s1[r * s1w + j]));
 #pragma unroll
-        for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
         const float s = m == 0.0f ? 1.0f : m / 127.0f;
         const float inv = 1.0f / s;
-        for (int j = l16; j < D.tv; j += 16)
+        for (int j = l32; j < D.tv; j += 32)
             pq[r * D.tv + j] = (r < nrows && j < t) ? q_code(s1[r * s1w + j], inv) : (int8_t)0;
         __syncthreads();  // the 1/sum of wave 0 is visible after this barrier
-        if (l16 == 0) rowv[32 + r] = s * rowv[16 + r];
+        if (l32 == 0) rowv[32 + r] = s * rowv[16 + r];
     }
     __syncthreads();
-    // context: channel blocks 2*wave, 2*wave+1; K over tv in 64-steps; A = pq rows from LDS, B = vT rows
-    // (the vT loads of kPF K steps of both blocks are issued before their MFMAs)
-    float val[2][4];
-    v4i pacc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+    // context: channel block `wave`; K over tv in 64-steps; A = pq rows from LDS, B = vT rows (the vT loads of
+    // kPF K steps are issued before their MFMAs)
+    float val[4];
+    v4i pacc = {0, 0, 0, 0};
     {
-        const int8_t *vr0 = W.vq + ((int64_t)h * kDh + 2 * wave * 16 + arow) * D.tv + 16 * aq;
-        const int8_t *vr1 = vr0 + (int64_t)16 * D.tv;
+        const int8_t *vr0 = W.vq + ((int64_t)h * kDh + wave * 16 + arow) * D.tv + 16 * aq;
         const int8_t *pr = pq + arow * D.tv + 16 * aq;
         for (int k0 = 0; k0 < D.tv; k0 += 64 * kPF) {
-            v4i b[2][kPF];
+            v4i b[kPF];
 #pragma unroll
-            for (int p = 0; p < kPF; p++) {
-                const int kk = min(k0 + 64 * p, D.tv - 64);
-                b[0][p] = *(const v4i *)(vr0 + kk);
-                b[1][p] = *(const v4i *)(vr1 + kk);
-            }
+            for (int p = 0; p < kPF; p++) b[p] = *(const v4i *)(vr0 + min(k0 + 64 * p, D.tv - 64));
 #pragma unroll
             for (int p = 0; p < kPF; p++) {
                 if (k0 + 64 * p < D.tv) {
                     const v4i a = *(const v4i *)(pr + k0 + 64 * p);
-                    pacc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[0][p], pacc[0], 0, 0, 0);
-                    pacc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[1][p], pacc[1], 0, 0, 0);
+                    pacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[p], pacc, 0, 0, 0);
                 }
             }
         }
     }
-#pragma unroll
-    for (int cbi = 0; cbi < 2; cbi++) {
-        const int cb = 2 * wave + cbi;
-        const v4i acc = pacc[cbi];
-        const int c = cb * 16 + dcol;
+    {
+        const int c = wave * 16 + dcol;
         const float vsv = W.vs[h * kDh + c];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int r = drow + e;
-            val[cbi][e] = __builtin_fmaf((float)acc[e], rowv[32 + r] * vsv, 0.0f);
-            if (!QOUT && r < nrows) ctx[(int64_t)(i0 + r) * D.d + h * kDh + c] = val[cbi][e];
+            val[e] = __builtin_fmaf((float)pacc[e], rowv[32 + r] * vsv, 0.0f);
+            if (!QOUT && r < nrows) ctx[(int64_t)(i0 + r) * D.d + h * kDh + c] = val[e];
         }
     }
     if constexpr (QOUT) {
-        // quantize_group of each query row over the head's 128 channels: 2 per lane, 16 lanes per wave, 4 waves
-        float *qmax = rowv + 64;       // [wave][row]
-        int *qsum = (int *)(rowv + 128);
+        // quantize_group of each query row over the head's 128 channels: one per lane, 16 lanes per wave, 8 waves
+        float *qmax = rowv + 64;         // [wave][row]
+        int *qsum = (int *)(rowv + 192);
         float sc[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            float m = fmaxf(fabsf(val[0][e]), fabsf(val[1][e]));
+            float m = fabsf(val[e]);
 #pragma unroll
             for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
             if (dcol == 0) qmax[wave * 16 + drow + e] = m;
@@ -376,16 +372,14 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int r = drow + e;
-            const float m = fmaxf(fmaxf(qmax[r], qmax[16 + r]), fmaxf(qmax[32 + r], qmax[48 + r]));
+            float m = qmax[r];
+#pragma unroll
+            for (int w = 1; w < NW; w++) m = fmaxf(m, qmax[w * 16 + r]);
             sc[e] = m == 0.0f ? 1.0f : m / 127.0f;
             const float inv = 1.0f / sc[e];
-            const int8_t c0 = q_code(val[0][e], inv), c1 = q_code(val[1][e], inv);
-            if (r < nrows) {
-                int8_t *qr = Q.q + (row0 + i0 + r) * D.d + h * kDh + 2 * wave * 16 + dcol;
-                qr[0] = c0;
-                qr[16] = c1;
-            }
-            int sum = (int)c0 + (int)c1;
+            const int8_t c0 = q_code(val[e], inv);
+            if (r < nrows) Q.q[(row0 + i0 + r) * D.d + h * kDh + wave * 16 + dcol] = c0;
+            int sum = (int)c0;
 #pragma unroll
             for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
             if (dcol == 0) qsum[wave * 16 + r] = sum;
@@ -397,8 +391,11 @@ __global__ __launch_bounds__(256) void attn_core_kernel(AttnDims D, AttnWs W, fl
                 const int r = drow + e;
                 if (r < nrows) {
                     const int64_t gi = (int64_t)h * Q.np + row0 + i0 + r;
+                    int g = 0;
+#pragma unroll
+                    for (int w = 0; w < NW; w++) g += qsum[w * 16 + r];
                     Q.s[gi] = sc[e];
-                    Q.g[gi] = qsum[r] + qsum[16 + r] + qsum[32 + r] + qsum[48 + r];
+                    Q.g[gi] = g;
                 }
             }
         }
@@ -495,9 +492,9 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
     AttnQOut Q{q, scales_t, gsum_t, (int)((nseg * t + 15) / 16 * 16)};
     const dim3 grid((unsigned)(D.tp / 16), (unsigned)h, (unsigned)nseg);
     if (qout)
-        attn_core_kernel<true><<<grid, 256, lds, st>>>(D, W, scaling, ctx, Q);
+        attn_core_kernel<true><<<grid, 64 * kCoreWaves, lds, st>>>(D, W, scaling, ctx, Q);
     else
-        attn_core_kernel<false><<<grid, 256, lds, st>>>(D, W, scaling, ctx, Q);
+        attn_core_kernel<false><<<grid, 64 * kCoreWaves, lds, st>>>(D, W, scaling, ctx, Q);
     hip_check(hipGetLastError(), "attention core kernel launch");
 }
 
