@@ -47,7 +47,8 @@ void attention_core_noalloc(const float *qkv, const float *rel_k, int64_t t, int
 void *static_attn_ws();
 void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
                         const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
-                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t, int64_t rel_ld);
+                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t, int64_t rel_ld,
+                        const int8_t *rq_pre, const float *rs_pre);
 void set_kernel_override(const char *name, const char *value);
 vx_encoder *encoder_create(const vx_encoder_config *cfg);
 void encoder_free(vx_encoder *e);
@@ -328,7 +329,7 @@ vx_status vx_attention_core_quantize(const float *qkv, const float *rel_k, int64
         vx::require(group == 128, "attention quantized output: 128-column groups (one per head)");
         vx::require(q && scales_t && gsum_t, "q, scales_t and gsum_t must not be NULL");
         vx::attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, ws, nullptr, (hipStream_t)stream, q,
-                               scales_t, gsum_t, d);
+                               scales_t, gsum_t, d, nullptr, nullptr);
     });
 }
 

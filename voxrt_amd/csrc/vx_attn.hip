@@ -73,6 +73,23 @@ __device__ inline float quant128(float a0, float a1, int lane, int8_t *dst) {
     return s;
 }
 
+// Relative row r of h * rp (head-major): row p of rel_k's block of head h quantized into rq [h][rp][dh], rs [h][rp];
+// rows past 2t-1 (the band's spare block) are zeros.
+__device__ inline void attn_rel_item(int r, const float *__restrict__ rel_k, const AttnDims &D, int8_t *rq,
+                                     float *rs) {
+    const int lane = threadIdx.x & 63;
+    if (r >= D.h * D.rp) return;
+    const int h = r / D.rp, p = r % D.rp;
+    float a0 = 0.0f, a1 = 0.0f;
+    if (p < D.np) {
+        const float2 v = *(const float2 *)(rel_k + (int64_t)p * D.rel_ld + h * kDh + 2 * lane);
+        a0 = v.x;
+        a1 = v.y;
+    }
+    const float s = quant128(a0, a1, lane, rq + ((int64_t)h * D.rp + p) * kDh);
+    if (lane == 0) rs[h * D.rp + p] = s;
+}
+
 // Work items: [0, nseg*h*tp) query/key rows (segment-major, then head-major), then h*rp relative rows (shared).
 __device__ inline void attn_rows_item(int item, const float *__restrict__ qkv, const float *__restrict__ rel_k,
                                       const float *__restrict__ bias_u, const float *__restrict__ bias_v,
@@ -107,17 +124,7 @@ __device__ inline void attn_rows_item(int item, const float *__restrict__ qkv, c
         }
         return;
     }
-    const int r = item - D.nseg * D.h * D.tp;
-    if (r >= D.h * D.rp) return;
-    const int h = r / D.rp, p = r % D.rp;
-    float a0 = 0.0f, a1 = 0.0f;
-    if (p < D.np) {
-        const float2 v = *(const float2 *)(rel_k + (int64_t)p * D.rel_ld + h * kDh + 2 * lane);
-        a0 = v.x;
-        a1 = v.y;
-    }
-    const float s = quant128(a0, a1, lane, W.rq + ((int64_t)h * D.rp + p) * kDh);
-    if (lane == 0) W.rs[h * D.rp + p] = s;
+    attn_rel_item(item - D.nseg * D.h * D.tp, rel_k, D, W.rq, W.rs);
 }
 
 // One wavefront per (segment, head, channel): vT row = v[i][h*dh + c] for i < t, zero to tv; one group.
@@ -136,6 +143,15 @@ __device__ inline void attn_vt_item(int item, const float *__restrict__ qkv, con
     int8_t *dst = W.vq + ((int64_t)item) * D.tv;
     for (int i = lane; i < D.tv; i += 64) dst[i] = i < D.t ? q_code(col[i * ld], inv) : (int8_t)0;
     if (lane == 0) W.vs[item] = s;
+}
+
+// The relative rows of nl layers in one launch (their projections depend on t and the weights only): layer blockIdx.y
+// reads columns [l*d, (l+1)*d) of rel_k (row pitch D.rel_ld) and writes rq + l * h*rp*dh, rs + l * h*rp.
+__global__ __launch_bounds__(256) void attn_rel_kernel(const float *__restrict__ rel_k, AttnDims D, int8_t *rq,
+                                                      float *rs) {
+    const int l = blockIdx.y;
+    attn_rel_item((int)blockIdx.x * 4 + (threadIdx.x >> 6), rel_k + (int64_t)l * D.d, D,
+                  rq + (int64_t)l * D.h * D.rp * kDh, rs + (int64_t)l * D.h * D.rp);
 }
 
 // The per-row quantizations and the vT rows in one launch: the first `rows_blocks` workgroups take the row items,
@@ -453,9 +469,11 @@ void attention_prime() {
 // groups (one per head): q int8 [nseg * t][d], scales_t and gsum_t [h][npad(nseg * t)].
 void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
                         const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
-                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t, int64_t rel_ld) {
-    const bool qout = q != nullptr;
-    require(qkv && rel_k && bias_u && bias_v && ws && (ctx || qout) && (!qout || (scales_t && gsum_t)),
+                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t, int64_t rel_ld,
+                        const int8_t *rq_pre, const float *rs_pre) {
+    const bool qout = q != nullptr, pre = rq_pre != nullptr;
+    require(qkv && (rel_k || pre) && bias_u && bias_v && ws && (ctx || qout) && (!qout || (scales_t && gsum_t)) &&
+                (!pre || rs_pre),
             "attention: NULL pointer");
     require(h > 0 && d == h * kDh, "attention: the head dimension must be 128");
     require(t >= 1 && t <= 1024, "attention: 1 <= t <= 1024 frames");
@@ -482,7 +500,11 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
     W.ks = (float *)take(rows * 4);
     W.rs = (float *)take(rrows * 4);
     W.vs = (float *)take((size_t)(nseg * h) * kDh * 4);
-    const int items = (int)(rows + rrows);
+    if (pre) {  // the relative rows were quantized by attention_rel_quantize
+        W.rq = const_cast<int8_t *>(rq_pre);
+        W.rs = const_cast<float *>(rs_pre);
+    }
+    const int items = (int)(rows + (pre ? 0 : rrows));
     const int rows_blocks = (items + 3) / 4, vt_blocks = (int)((nseg * h * kDh + 3) / 4);
     attn_prep_kernel<<<(unsigned)(rows_blocks + vt_blocks), 256, 0, st>>>(qkv, rel_k, bias_u, bias_v, D, W,
                                                                          rows_blocks);
@@ -496,6 +518,23 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
     else
         attn_core_kernel<false><<<grid, 64 * kCoreWaves, lds, st>>>(D, W, scaling, ctx, Q);
     hip_check(hipGetLastError(), "attention core kernel launch");
+}
+
+// The relative rows of nl layers quantized once, for attention_core_seg's rq_pre / rs_pre: layer l's rows are
+// columns [l*d, (l+1)*d) of rel_k [2t-1][rel_ld]; per layer rq holds attn_rel_rows(t, h) rows of dh int8 ([h][rp][dh])
+// and rs attn_rel_rows(t, h) floats ([h][rp]).
+int64_t attn_rel_rows(int64_t t, int64_t h) { return h * AttnDims((int)t, (int)(h * kDh), (int)h).rp; }
+
+void attention_rel_quantize(const float *rel_k, int64_t nl, int64_t t, int64_t d, int64_t h, int64_t rel_ld,
+                            int8_t *rq, float *rs, hipStream_t st) {
+    require(rel_k && rq && rs, "attention relative rows: NULL pointer");
+    require(h > 0 && d == h * kDh && t >= 1 && t <= 1024 && nl >= 1 && nl <= 65535, "attention relative rows: shape");
+    require(rel_ld >= nl * d && (2 * t - 1) * rel_ld < (1ll << 31), "attention relative rows: bad rel_k row pitch");
+    AttnDims D((int)t, (int)d, (int)h);
+    D.rel_ld = (int)rel_ld;
+    const dim3 grid((unsigned)((h * D.rp + 3) / 4), (unsigned)nl);
+    attn_rel_kernel<<<grid, 256, 0, st>>>(rel_k, D, rq, rs);
+    hip_check(hipGetLastError(), "attention relative rows kernel launch");
 }
 
 // ---------------------------------------------------------------- the attention core without a caller workspace
@@ -538,13 +577,14 @@ void attention_core_noalloc(const float *qkv, const float *rel_k, int64_t t, int
                                             " bytes of workspace, above the fixed " +
                                             std::to_string(kStaticAttnWsBytes) + " (use vx_attention_core)");
     attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, static_attn_ws(), ctx, st, nullptr, nullptr,
-                       nullptr, d);
+                       nullptr, d, nullptr, nullptr);
 }
 
 // ctx [t][d] from qkv [t][3d] (q | k | v) and rel_k [2t-1][d]; ws is attn_ws_bytes(t, d, h) device bytes.
 void attention_core(const float *qkv, const float *rel_k, int64_t t, int64_t d, int64_t h, const float *bias_u,
                     const float *bias_v, float scaling, void *ws, float *ctx, hipStream_t st) {
-    attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, ws, ctx, st, nullptr, nullptr, nullptr, d);
+    attention_core_seg(qkv, rel_k, 1, t, d, h, bias_u, bias_v, scaling, ws, ctx, st, nullptr, nullptr, nullptr, d,
+                       nullptr, nullptr);
 }
 
 }  // namespace vx

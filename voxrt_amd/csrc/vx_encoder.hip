@@ -67,7 +67,11 @@ void attention_prime();
 int cu_count();
 void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int64_t t, int64_t d, int64_t h,
                         const float *bias_u, const float *bias_v, float scaling, void *ws, float *ctx,
-                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t, int64_t rel_ld);
+                        hipStream_t st, int8_t *q, float *scales_t, int32_t *gsum_t, int64_t rel_ld,
+                        const int8_t *rq_pre, const float *rs_pre);
+int64_t attn_rel_rows(int64_t t, int64_t h);
+void attention_rel_quantize(const float *rel_k, int64_t nl, int64_t t, int64_t d, int64_t h, int64_t rel_ld,
+                            int8_t *rq, float *rs, hipStream_t st);
 
 constexpr int64_t kMaxFrames = 1024;  // frames per segment (the attention core's limit)
 constexpr int64_t kMaxRows = 65535;   // segments * frames in one call
@@ -145,11 +149,11 @@ struct EncWs {
     int64_t rows = 0, np = 0;
     size_t attn_bytes = 0;
     int64_t sub_floats = 0;
-    DevBuf x[2], hbuf, qkv, rel_k, ctx, g2, hb, attn, sub_scratch;
+    DevBuf x[2], hbuf, qkv, rel_k, relq, rels, ctx, g2, hb, attn, sub_scratch;
     QBuf a, f, posq;
     size_t bytes() const {
-        return x[0].bytes + x[1].bytes + hbuf.bytes + qkv.bytes + rel_k.bytes + ctx.bytes + g2.bytes + hb.bytes +
-               attn.bytes + sub_scratch.bytes + a.bytes() + f.bytes() + posq.bytes();
+        return x[0].bytes + x[1].bytes + hbuf.bytes + qkv.bytes + rel_k.bytes + relq.bytes + rels.bytes + ctx.bytes +
+               g2.bytes + hb.bytes + attn.bytes + sub_scratch.bytes + a.bytes() + f.bytes() + posq.bytes();
     }
 };
 
@@ -269,8 +273,15 @@ void ensure_workspace(vx_encoder *e, int64_t t, int64_t nseg, int64_t sub_floats
     if (g_np) {
         const int64_t n = grown(np, 2 * kMaxFrames - 1);
         w.rel_k = DevBuf();
+        w.relq = DevBuf();
+        w.rels = DevBuf();
         w.posq = QBuf();
         w.rel_k = DevBuf((size_t)(n * c.n_layers * c.d) * f4);  // [np][n_layers * d]: every layer's projection
+        // every layer's relative rows quantized for the attention: [n_layers][heads][rp][128] int8 and
+        // [n_layers][heads][rp] scales, rp = up16(np) + 16 at this capacity
+        const int64_t rrows = c.heads * ((n + 15) / 16 * 16 + 16);
+        w.relq = DevBuf((size_t)(c.n_layers * rrows * (c.d / c.heads)));
+        w.rels = DevBuf((size_t)(c.n_layers * rrows) * f4);
         w.posq.alloc(n, c.d, c.group);
         w.np = n;
     }
@@ -309,8 +320,12 @@ void run_layers(vx_encoder *e, int64_t t_seg, int64_t nseg, hipStream_t st, Prof
     // rel_k [np][n_layers * d], layer l's block at columns [l*d, (l+1)*d)
     quantize_ln(e->pos_table.as<float>() + (kMaxFrames - t_seg) * d, np, d, G, nullptr, nullptr, w.posq.q.as<int8_t>(),
                 w.posq.s.as<float>(), w.posq.g.as<int32_t>(), st);
-    const int64_t rel_ld = (int64_t)e->layers.size() * d;
+    const int64_t rel_ld = (int64_t)e->layers.size() * d, nl = (int64_t)e->layers.size();
     gemm_full(e->pos_all, w.posq, np, w.rel_k.as<float>(), VX_EP_STORE, 0.0f, st);
+    // and the attention's quantization of those rows, for all layers in one launch
+    const int64_t rrows = attn_rel_rows(t_seg, c.heads), dh = d / c.heads;
+    attention_rel_quantize(w.rel_k.as<float>(), nl, t_seg, d, c.heads, rel_ld, w.relq.as<int8_t>(),
+                           w.rels.as<float>(), st);
     mark(kProfAttn);
     for (size_t li = 0; li < e->layers.size(); li++) {
         EncLayer &L = *e->layers[li];
@@ -344,12 +359,14 @@ void run_layers(vx_encoder *e, int64_t t_seg, int64_t nseg, hipStream_t st, Prof
         if (G == 128) {  // a head's 128 channels are one group: the core writes the o-projection's activations
             attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>() + li * d, nseg, t_seg, d, c.heads,
                                L.bias_u.as<float>(), L.bias_v.as<float>(), scaling, w.attn.p, nullptr, st,
-                               w.a.q.as<int8_t>(), w.a.s.as<float>(), w.a.g.as<int32_t>(), rel_ld);
+                               w.a.q.as<int8_t>(), w.a.s.as<float>(), w.a.g.as<int32_t>(), rel_ld,
+                               w.relq.as<int8_t>() + li * rrows * dh, w.rels.as<float>() + li * rrows);
             mark(kProfAttnCore);
         } else {
             attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>() + li * d, nseg, t_seg, d, c.heads,
                                L.bias_u.as<float>(), L.bias_v.as<float>(), scaling, w.attn.p, w.ctx.as<float>(), st,
-                               nullptr, nullptr, nullptr, rel_ld);
+                               nullptr, nullptr, nullptr, rel_ld, w.relq.as<int8_t>() + li * rrows * dh,
+                               w.rels.as<float>() + li * rrows);
             mark(kProfAttnCore);
             quant(w.ctx.as<float>(), d, w.a);
         }
