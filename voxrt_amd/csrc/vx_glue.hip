@@ -490,6 +490,79 @@ __global__ __launch_bounds__(256) void dwconv2d_kernel(const float *__restrict__
     }
 }
 
+// Stage 0 and the first depthwise stage in one pass, without the stage-0 tensor in memory, for the model's shape (3x3
+// kernels, stride 2, NM mel bins: F1 = NM / 2 stage-0 frequencies, F2 = F1 / 2 depthwise outputs). A block is one
+// output time row ot2 of the depthwise stage, a thread one channel: it streams the stage-0 values of its channel
+// over the input rows it = 2 ot2 + kt - 1 (kt ascending, in range) and, within a row, the frequencies in ascending
+// order, each recomputed exactly as conv0_kernel does (taps in order, ReLU), and adds each into the depthwise
+// outputs it feeds (of2 with 2 of2 + kf - 1 = i_f). For every depthwise output this visits its in-range taps in the
+// reference's order (kt outer, kf inner), so the sums equal conv0_kernel followed by dwconv2d_kernel bit for bit.
+// The three input rows of each stage-0 row are staged in LDS.
+template <int NM>
+__global__ __launch_bounds__(256) void conv0_dw_kernel(const float *__restrict__ feats, int t,
+                                                      const float *__restrict__ w0, const float *__restrict__ b0,
+                                                      const float *__restrict__ w1, const float *__restrict__ b1,
+                                                      int c, int t1, int t2, float *__restrict__ y) {
+    constexpr int F1 = NM / 2, F2 = F1 / 2;
+    static_assert(NM % 4 == 0, "two stride-2 halvings without a remainder");
+    __shared__ float rows[3][3][NM];  // [stage-0 row kt][its input row kt0][mel bin]
+    const int ot2 = blockIdx.x % t2, seg = blockIdx.x / t2;
+    feats += (int64_t)seg * t * NM;
+    y += (int64_t)seg * t2 * F2 * c;
+    for (int e = threadIdx.x; e < 9 * NM; e += blockDim.x) {
+        const int kt = e / (3 * NM), kt0 = (e / NM) % 3, f = e % NM;
+        const int it = 2 * ot2 + kt - 1, ii = 2 * it + kt0 - 1;
+        rows[kt][kt0][f] = (it >= 0 && it < t1 && ii >= 0 && ii < t) ? feats[(int64_t)ii * NM + f] : 0.0f;
+    }
+    __syncthreads();
+    for (int ch = threadIdx.x; ch < c; ch += blockDim.x) {
+        float wa[9], wb[9];
+#pragma unroll
+        for (int i = 0; i < 9; i++) {
+            wa[i] = w0[i * c + ch];
+            wb[i] = w1[i * c + ch];
+        }
+        const float bc0 = b0[ch];
+        float acc[F2];
+#pragma unroll
+        for (int o = 0; o < F2; o++) acc[o] = b1[ch];
+        for (int kt = 0; kt < 3; kt++) {
+            const int it = 2 * ot2 + kt - 1;
+            if (it < 0 || it >= t1) continue;
+            bool in_row[3];
+#pragma unroll
+            for (int kt0 = 0; kt0 < 3; kt0++) {
+                const int ii = 2 * it + kt0 - 1;
+                in_row[kt0] = ii >= 0 && ii < t;
+            }
+            const float *r0 = rows[kt][0], *r1 = rows[kt][1], *r2 = rows[kt][2];
+#pragma unroll
+            for (int i_f = 0; i_f < F1; i_f++) {
+                // the stage-0 value (it, i_f) of this channel: taps (kt0, kf0) in order, bins 2 i_f + kf0 - 1
+                float o = bc0;
+#pragma unroll
+                for (int kt0 = 0; kt0 < 3; kt0++) {
+                    if (!in_row[kt0]) continue;
+                    const float *r = kt0 == 0 ? r0 : kt0 == 1 ? r1 : r2;
+#pragma unroll
+                    for (int kf0 = 0; kf0 < 3; kf0++) {
+                        const int fi = 2 * i_f + kf0 - 1;
+                        if (fi < 0 || fi >= NM) continue;
+                        o = o + wa[kt0 * 3 + kf0] * r[fi];
+                    }
+                }
+                o = o > 0.0f ? o : 0.0f;
+                // into the depthwise outputs it feeds, in ascending kf
+                if (i_f % 2 == 1 && (i_f + 1) / 2 < F2) acc[(i_f + 1) / 2] = acc[(i_f + 1) / 2] + wb[kt * 3 + 0] * o;
+                if (i_f % 2 == 0) acc[i_f / 2] = acc[i_f / 2] + wb[kt * 3 + 1] * o;
+                if (i_f % 2 == 1) acc[(i_f - 1) / 2] = acc[(i_f - 1) / 2] + wb[kt * 3 + 2] * o;
+            }
+        }
+#pragma unroll
+        for (int o = 0; o < F2; o++) y[((int64_t)ot2 * F2 + o) * c + ch] = acc[o];
+    }
+}
+
 // The whole subsampling (subsampling.rs:124-204) of nseg segments of t frames each on device buffers: feats
 // [nseg][t][nm] -> out [nseg][t3][d_model]; scratch must hold 2 * nseg * t1 * f1 * c floats. Returns t3.
 int64_t subsampling_seg(const float *feats, int64_t nseg, int64_t t, int64_t nm, int64_t c, int64_t k, int64_t s,
@@ -504,16 +577,27 @@ int64_t subsampling_seg(const float *feats, int64_t nseg, int64_t t, int64_t nm,
     const int t1 = conv_out_len((int)t, (int)k, (int)s, p), f1 = conv_out_len((int)nm, (int)k, (int)s, p);
     require(nseg >= 1 && nseg * t1 * f1 * c < (1ll << 31), "subsampling: input too long");
     float *a = scratch, *bbuf = scratch + nseg * t1 * f1 * c;
-    conv0_kernel<<<(unsigned)(nseg * t1), 256, 0, st>>>(feats, (int)t, (int)nm, (int)k, (int)s, conv0_w,
-                                                                conv0_b, (int)c, t1, f1, a);
-    hip_check(hipGetLastError(), "conv0 kernel launch");
+    // the model's shape (3x3, stride 2, 128 mel bins) runs stage 0 inside the first depthwise stage
+    const bool fused = k == 3 && s == 2 && nm == 128;
+    if (!fused) {
+        conv0_kernel<<<(unsigned)(nseg * t1), 256, 0, st>>>(feats, (int)t, (int)nm, (int)k, (int)s, conv0_w,
+                                                                    conv0_b, (int)c, t1, f1, a);
+        hip_check(hipGetLastError(), "conv0 kernel launch");
+    }
     int tc = t1, fc = f1;
     for (int stage = 0; stage < 2; stage++) {
         const int t2 = conv_out_len(tc, (int)k, (int)s, p), f2 = conv_out_len(fc, (int)k, (int)s, p);
-        dwconv2d_kernel<<<(unsigned)(nseg * t2 * f2), 256, 0, st>>>(a, tc, fc, (int)k, (int)s,
-                                                                      dw_w + (int64_t)stage * k * k * c,
-                                                                      dw_b + (int64_t)stage * c, (int)c, t2, f2, bbuf);
-        hip_check(hipGetLastError(), "dwconv2d kernel launch");
+        if (stage == 0 && fused) {
+            conv0_dw_kernel<128><<<(unsigned)(nseg * t2), 256, 0, st>>>(feats, (int)t, conv0_w, conv0_b, dw_w, dw_b,
+                                                                         (int)c, t1, t2, bbuf);
+            hip_check(hipGetLastError(), "conv0 + dwconv2d kernel launch");
+        } else {
+            dwconv2d_kernel<<<(unsigned)(nseg * t2 * f2), 256, 0, st>>>(a, tc, fc, (int)k, (int)s,
+                                                                          dw_w + (int64_t)stage * k * k * c,
+                                                                          dw_b + (int64_t)stage * c, (int)c, t2, f2,
+                                                                          bbuf);
+            hip_check(hipGetLastError(), "dwconv2d kernel launch");
+        }
         linear_f32(bbuf, nseg * t2 * f2, c, pw_w + (int64_t)stage * c * c, pw_b + (int64_t)stage * c, c, a, true,
                    st);
         tc = t2;
