@@ -119,11 +119,12 @@ def test_kernel_override_is_explicit_and_checked():
     L = vx.lib()
     for name, value in [("gemm", b"stream"), ("gemm", b"small"), ("tile", b"2x4"), ("small_tile", b"1x8"),
                         ("stream_grid", b"16"), ("small_ws", b"on"), ("small_ws", b"off"), ("linear", b"lds"),
-                        ("linear", b"mfma2x2")]:
+                        ("linear", b"mfma2x2"), ("stream_tile", b"4")]:
         assert L.vx_set_kernel_override(name.encode(), value) == 0
         assert L.vx_set_kernel_override(name.encode(), None) == 0
     for name, value in [(b"gemm", b"fastest"), (b"tile", b"2by4"), (b"stream_grid", b"12"), (b"grid", b"8"),
-                        (b"small_ws", b"yes"), (b"linear", b"3")]:
+                        (b"small_ws", b"yes"), (b"linear", b"3"),
+                        (b"stream_tile", b"6")]:
         assert L.vx_set_kernel_override(name, value) == kernels.VX_ERR_INVALID
     with kernels.kernel_override(gemm="direct", tile="1x2"):
         pass

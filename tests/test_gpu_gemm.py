@@ -444,13 +444,14 @@ def test_stream_kernel_every_output(dev, orc, m, k, n_out, grid):
                                                          f"bias={with_bias}")
 
 
+@pytest.mark.parametrize("tile", ["8", "4"])
 @pytest.mark.parametrize("m,k,n_out,grid", [(1536, 1024, 2048, 16), (1536 + 37, 1024, 1024, 8),
                                             (1024, 4096, 1024, 8), (2048, 1024, 3072, 0)])
-def test_stream_groups_kernel_every_output(dev, orc, m, k, n_out, grid):
+def test_stream_groups_kernel_every_output(dev, orc, m, k, n_out, grid, tile):
     """The streaming kernel for 128-column groups (the model format: f16 scales per row and group, per-token and
     group activation scales), forced on shapes the oracle checks in full: several tiles per workgroup, K = 4096
-    (32 groups), a ragged token count whose last 37 rows go through another kernel; each epilogue with and without
-    bias, every output bit-exact."""
+    (32 groups), a ragged token count whose last 37 rows go through another kernel; 128-token tiles (one
+    workgroup per CU) and 64-token tiles (two); each epilogue with and without bias, every output bit-exact."""
     import voxrt_amd as vx
 
     group = 128
@@ -462,7 +463,7 @@ def test_stream_groups_kernel_every_output(dev, orc, m, k, n_out, grid):
     rng = synth.Lcg(43)
     base = ((rng.take(m * n_out) % 200).astype(np.float32) * np.float32(0.01) - np.float32(1.0)).reshape(m, n_out)
     bias = (rng.take(n_out) % 100).astype(np.float32) / np.float32(10.0)
-    with vx.kernels.kernel_override(gemm="stream", stream_grid=grid or None):
+    with vx.kernels.kernel_override(gemm="stream", stream_grid=grid or None, stream_tile=tile):
         for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
             want = orc.gemm(trits, ws, q, xs, group, y=base.copy(), ep=ep_kind, alpha=alpha)
             for with_bias in (False, True):

@@ -74,6 +74,7 @@ enum ForcedKernel { kForceNone, kForceDirect, kForceSplitK, kForceLds, kForceBig
 struct KernelOverrides {
     std::atomic<int> gemm{kForceNone}, tile{0}, small_tile{0}, stream_grid{0};
     std::atomic<int> small_ws{0};  // grouped small-token kernel with producer/consumer wavefronts: 0 auto, 1 on, 2 off
+    std::atomic<int> stream_tb{0}; // 128-column-group streaming kernel: token blocks per wavefront (4 or 8), 0 auto
     std::atomic<int> linear{0};    // f32 linear: 0 auto, -1 the LDS-broadcast kernel, 1WT*10+WO the matrix-core
                                    // kernel with WT x WO blocks per wavefront (111, 121, 122)
 };

@@ -634,8 +634,8 @@ __global__ __launch_bounds__(256) void tgemm_splitk_kernel(const GemmArgs a) {
             r[j] = ep_apply(a.ep, a.alpha, old[j], v[j]);
             if (a.bias) r[j] = r[j] + bia[j];
         }
-        *(float4 *)(yrow + o0) = make_float4(r[0], r[1], r[2], r[3]);
-        *(float4 *)(yrow + o0 + 4) = make_float4(r[4], r[5], r[6], r[7]);
+        store16_sep((float4 *)(yrow + o0), make_float4(r[0], r[1], r[2], r[3]));
+        store16_sep((float4 *)(yrow + o0 + 4), make_float4(r[4], r[5], r[6], r[7]));
     } else {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -811,8 +811,8 @@ __global__ __launch_bounds__(256) void tgemm_splitk_groups_kernel(const GemmArgs
             r[j] = ep_apply(a.ep, a.alpha, old[j], v[j]);
             if (a.bias) r[j] = r[j] + bia[j];
         }
-        *(float4 *)(yrow + o0) = make_float4(r[0], r[1], r[2], r[3]);
-        *(float4 *)(yrow + o0 + 4) = make_float4(r[4], r[5], r[6], r[7]);
+        store16_sep((float4 *)(yrow + o0), make_float4(r[0], r[1], r[2], r[3]));
+        store16_sep((float4 *)(yrow + o0 + 4), make_float4(r[4], r[5], r[6], r[7]));
     } else {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -1362,7 +1362,8 @@ KernelOverrides &overrides() {
 // vx_set_kernel_override: name "gemm" (direct, splitk, lds, big, splitg, small, stream), "tile" and "small_tile"
 // ("MTxNT"), "stream_grid" (workgroups, a multiple of 8), "small_ws" ("on" / "off": the grouped small-token kernel
 // with producer and consumer wavefronts), "linear" (the f32 linear: "lds", or the
-// matrix-core kernel's tile, "mfma1x1" / "mfma2x1" / "mfma2x2"); NULL or "" clears the name's override.
+// matrix-core kernel's tile, "mfma1x1" / "mfma2x1" / "mfma2x2"), "stream_tile" (token blocks of 16 per wavefront of
+// the 128-column-group streaming kernel: 4 or 8); NULL or "" clears the name's override.
 void set_kernel_override(const char *name, const char *value) {
     require(name != nullptr, "override name must not be NULL");
     const std::string n(name), v(value ? value : "");
@@ -1388,6 +1389,10 @@ void set_kernel_override(const char *name, const char *value) {
     } else if (n == "small_ws") {
         require(v.empty() || v == "on" || v == "off", "small_ws is \"on\", \"off\" or empty");
         o.small_ws.store(v.empty() ? 0 : v == "on" ? 1 : 2, std::memory_order_relaxed);
+    } else if (n == "stream_tile") {
+        const int tb = v.empty() ? 0 : atoi(v.c_str());
+        require(tb == 0 || tb == 4 || tb == 8, "stream_tile is 4, 8 or empty");
+        o.stream_tb.store(tb, std::memory_order_relaxed);
     } else if (n == "linear") {
         const int k = v.empty() ? 0 : v == "lds" ? -1 : v == "mfma1x1" ? 111 : v == "mfma2x1" ? 121
                                                         : v == "mfma2x2" ? 122 : -2;

@@ -328,11 +328,11 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
             }
         } else if (t >= a.t0 && t < a.t1 && (BM % RPP == 0 || tt0 + r * RPP < BM)) {
             const uint32_t so = (uint32_t)t * out4 + (uint32_t)o0 * 4;
-            __builtin_amdgcn_raw_buffer_store_b128(lo, yrs, so, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(hi, yrs, so + 16, 0, 0);
+            store_b128_sep(lo, yrs, so, 0);
+            store_b128_sep(hi, yrs, so + 16, 0);
             if constexpr (GSO) {
-                __builtin_amdgcn_raw_buffer_store_b128(gso[r][0], gsrs, so, 0, 0);
-                __builtin_amdgcn_raw_buffer_store_b128(gso[r][1], gsrs, so + 16, 0, 0);
+                store_b128_sep(gso[r][0], gsrs, so, 0);
+                store_b128_sep(gso[r][1], gsrs, so + 16, 0);
             }
         }
     }
@@ -571,8 +571,8 @@ __global__ __launch_bounds__(512, NPL == 1 ? 2 : 1) void tgemm_small_ws_kernel(c
             }
         } else if (t >= a.t0 && t < a.t1 && (BM % RPP == 0 || tt0 + r * RPP < BM)) {
             const uint32_t so = (uint32_t)t * out4 + (uint32_t)o0 * 4;
-            __builtin_amdgcn_raw_buffer_store_b128(lo, yrs, so, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(hi, yrs, so + 16, 0, 0);
+            store_b128_sep(lo, yrs, so, 0);
+            store_b128_sep(hi, yrs, so + 16, 0);
         }
     }
 }

@@ -213,8 +213,8 @@ __global__ __launch_bounds__(256, OCC2 ? 2 : 1) void tgemm_stream_kernel(const G
     // be merged into one by the compiler, and the wait counts, which assume two, would no longer cover the loads.
     auto dummy_stores = [&]() {
         const v4i z{0, 0, 0, 0};
-        __builtin_amdgcn_raw_buffer_store_b128(z, yrs, kOff, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(z, yrs, kOff - 16, 0, 0);
+        store_b128_sep(z, yrs, kOff, 0);
+        store_b128_sep(z, yrs, kOff - 16, 0);
     };
     auto out_block = [&](const v4i (&acc)[8][4], const BlockScales &c, int tb, int ob, uint32_t vy, uint32_t sy) {
         const float xs = c.xs;
@@ -240,8 +240,8 @@ __global__ __launch_bounds__(256, OCC2 ? 2 : 1) void tgemm_stream_kernel(const G
             if constexpr (BIAS) res = res + bv[e];
             r[e] = __float_as_int(res);
         }
-        __builtin_amdgcn_raw_buffer_store_b128(r, yrs, vy, so, 0);
-        if constexpr (GSO) __builtin_amdgcn_raw_buffer_store_b128(sums, gsrs, vy, so, 0);
+        store_b128_sep(r, yrs, vy, so);
+        if constexpr (GSO) store_b128_sep(sums, gsrs, vy, so);
     };
 
     // one K step. i: tile step (runtime in the middle loop); SLOT = i % 8 (LDS slot);

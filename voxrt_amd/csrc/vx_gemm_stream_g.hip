@@ -4,7 +4,8 @@
 //   acc = 0; for each group g ascending: acc = fma((float)S_g, xs[t][g] * ws[o][g], acc); y = ep(acc) (+ bias)
 //
 // Tiles, XCD grouping, MFMA operand roles and the load pipeline are those of the one-group streaming kernel
-// (vx_gemm_stream.hip): 128-token x 256-row tiles, wavefront w owns rows [64w, 64w + 64) and all 128 tokens,
+// (vx_gemm_stream.hip): 128-token (or 64-token, two workgroups per CU) x 256-row tiles, wavefront w owns rows
+// [64w, 64w + 64) and all the tile's tokens,
 // v_mfma_i32_16x16x64_i8 with A = weight codes and B = activations, the activation tile and the weight codes of
 // step s + 6 brought to LDS by buffer_load ... lds, one constant vmcnt wait and one barrier per step.
 //
@@ -23,10 +24,11 @@ namespace vx {
 namespace {
 
 constexpr int kPDg = 6;  // steps of loads in flight
-// Per step 4 vector-memory instructions (2 activation DMA, 1 weight DMA, 1 scale DMA) issued together. When step
-// s begins, the loads of step s+1 (issued at step s+1-kPDg) must be complete: the instructions issued after them
-// are those of steps s+2-kPDg .. s-1.
-constexpr int kWaitG = 4 * (kPDg - 2);
+// Per step TB / 4 + 2 vector-memory instructions per wavefront (TB / 4 activation DMA, 1 weight DMA, 1 scale DMA)
+// issued together. When step s begins, the loads of step s+1 (issued at step s+1-kPDg) must be complete: the
+// instructions issued after them are those of steps s+2-kPDg .. s-1.
+__host__ __device__ constexpr int vmem_per_step(int tb) { return tb / 4 + 2; }
+__host__ __device__ constexpr int wait_g(int tb) { return vmem_per_step(tb) * (kPDg - 2); }
 
 // 16 weight codes (trit + 1, 2 bits each, in the MFMA operand order) -> 16 signed trits: byte b of component d is
 // code 4d + b; v_perm_b32 with the codes as byte selectors picks -1, 0, +1 from the table 0x000100FF.
@@ -39,12 +41,17 @@ __device__ inline v4i widen_trits(uint32_t p) {
     return r;
 }
 
-template <int EP, bool BIAS>
-__global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmArgs a, const StreamGeom g) {
+// TB: token blocks of 16 per wavefront, the tile's token rows are 16 TB. TB = 8: one workgroup per CU (128-token
+// tiles); TB = 4: 64-token tiles, half the accumulators and LDS, two workgroups (two wavefronts per SIMD) per CU, so
+// that one wavefront's fold issues while the other's MFMAs run.
+template <int EP, bool BIAS, int TB>
+__global__ __launch_bounds__(256, TB == 4 ? 2 : 1) void tgemm_stream_groups_kernel(const GemmArgs a,
+                                                                                    const StreamGeom g) {
     typedef __attribute__((address_space(3))) void lds_void;
+    constexpr int BM = 16 * TB, NAD = TB / 4;  // tile token rows; activation DMAs (16 rows each) per wavefront
     // one LDS object per slot, so that the compiler sees that a DMA into one slot does not alias reads of another
-    __shared__ __attribute__((aligned(1024))) int8_t sa0[8192], sa1[8192], sa2[8192], sa3[8192], sa4[8192],
-        sa5[8192], sa6[8192], sa7[8192];
+    __shared__ __attribute__((aligned(1024))) int8_t sa0[BM * 64], sa1[BM * 64], sa2[BM * 64], sa3[BM * 64],
+        sa4[BM * 64], sa5[BM * 64], sa6[BM * 64], sa7[BM * 64];
     __shared__ __attribute__((aligned(1024))) uint32_t sw0[1024], sw1[1024], sw2[1024], sw3[1024], sw4[1024],
         sw5[1024], sw6[1024], sw7[1024];
     // per group slot: token scales (256 tokens from the tile's first, 128 used), weight scales (256 rows)
@@ -76,35 +83,37 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmA
     const auto wsrs = make_rsrc(a.ws_t, a.ws_bytes);
     const auto yrs = make_rsrc(a.y, a.y_bytes);
 
-    uint32_t vdma[2];
+    uint32_t vdma[NAD];
     {
         const int i = lane >> 2, c = (lane & 3) ^ ((i >> 2) & 3);
 #pragma unroll
-        for (int q = 0; q < 2; q++) vdma[q] = (uint32_t)(((2 * wave + q) * 16 + i) * inp + c * 16);
+        for (int q = 0; q < NAD; q++) vdma[q] = (uint32_t)(((NAD * wave + q) * 16 + i) * inp + c * 16);
     }
     const uint32_t vfr = (uint32_t)(l16 * 64 + ((lq ^ ((l16 >> 2) & 3)) * 16));
     const uint32_t vwd = (uint32_t)((lane >> 4) * nk * 256 + (lane & 15) * 16);
     const uint32_t vyl = (uint32_t)l16 * out4 + (uint32_t)lq * 16;
-    const uint32_t vl16 = (uint32_t)lane * 16;
+    const uint32_t vq4 = (uint32_t)(64 * wave + lane) * 4;  // this wavefront's quarter of a scale table
 
     // --- tile state ---------------------------------------------------------------------------------------------
     int jt = 0;
     int cur = tile_at(0);
     if (cur < 0) return;  // a workgroup of the last XCD past its last tile
-    int m0 = (cur / g.n_nt) * kBM, n0 = (cur % g.n_nt) * kBN;
+    int m0 = (cur / g.n_nt) * BM, n0 = (cur % g.n_nt) * kBN;
     uint32_t sa_cur = (uint32_t)m0 * inp, sw_cur = (uint32_t)((n0 / 16 + wave * 4) * nk) * 256;
-    uint32_t sa_nxt = 0, sw_nxt = 0, vdma_nxt[2] = {kOff, kOff}, vw_nxt = kOff;
+    uint32_t sa_nxt = 0, sw_nxt = 0, vdma_nxt[NAD], vw_nxt = kOff;
+#pragma unroll
+    for (int q = 0; q < NAD; q++) vdma_nxt[q] = kOff;
     int nxt = -1, nm0 = 0, nn0 = 0;
     bool has_nxt = false;
     auto set_next = [&]() __attribute__((always_inline)) {
         nxt = tile_at(jt + 1);
         has_nxt = nxt >= 0;
-        nm0 = has_nxt ? (nxt / g.n_nt) * kBM : 0;
+        nm0 = has_nxt ? (nxt / g.n_nt) * BM : 0;
         nn0 = has_nxt ? (nxt % g.n_nt) * kBN : 0;
         sa_nxt = (uint32_t)nm0 * inp;
         sw_nxt = (uint32_t)((nn0 / 16 + wave * 4) * nk) * 256;
-        vdma_nxt[0] = has_nxt ? vdma[0] : kOff;
-        vdma_nxt[1] = has_nxt ? vdma[1] : kOff;
+#pragma unroll
+        for (int q = 0; q < NAD; q++) vdma_nxt[q] = has_nxt ? vdma[q] : kOff;
         vw_nxt = has_nxt ? vwd : kOff;
     };
 
@@ -112,29 +121,30 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmA
     // activations, weight codes, and the scales of group k / 2 (even k: token scales; odd k: weight scales)
     // (slot, the group slot q = (k / 2) % 4 and the parity of k are compile-time at every call: tile steps run in
     // blocks of 8 aligned to multiples of 8)
-    auto loads = [&](int slot, int q, int odd, int k, bool live, const uint32_t (&vd)[2], uint32_t sa, uint32_t vw,
+    auto loads = [&](int slot, int q, int odd, int k, bool live, const uint32_t *vd, uint32_t sa, uint32_t vw,
                      uint32_t sw, int tm0, int tn0) {
 #pragma unroll
-        for (int q = 0; q < 2; q++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(sact(slot) + (2 * wave + q) * 1024), 16,
+        for (int q = 0; q < NAD; q++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(sact(slot) + (NAD * wave + q) * 1024), 16,
                                                      vd[q], sa + (uint32_t)k * 64, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void *)(swt(slot) + wave * 256), 16, vw,
                                                  sw + (uint32_t)k * 256, 0, 0);
+        // the group's scales, each wavefront one quarter of the 256-entry table (4 bytes per lane)
         const int gg = k >> 1;
         if (!odd) {
-            const uint32_t vt = live ? (uint32_t)gg * np4 + (uint32_t)tm0 * 4 + vl16 : kOff;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_void *)sxs(q), 16, vt, 0, 0, 0);
+            const uint32_t vt = live ? (uint32_t)gg * np4 + (uint32_t)tm0 * 4 + vq4 : kOff;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_void *)(sxs(q) + 64 * wave), 4, vt, 0, 0, 0);
         } else {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wsrs, (lds_void *)sws(q), 16, live ? vl16 : kOff,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wsrs, (lds_void *)(sws(q) + 64 * wave), 4, live ? vq4 : kOff,
                                                      (uint32_t)gg * opad4 + (uint32_t)tn0 * 4, 0, 0);
         }
     };
 
-    v4i fr[2][8];
+    v4i fr[2][TB];
     uint32_t rw[4];
     auto read_frags = [&](int slot, int set) __attribute__((always_inline)) {
 #pragma unroll
-        for (int tb = 0; tb < 8; tb++) fr[set][tb] = *(const v4i *)(sact(slot) + tb * 1024 + vfr);
+        for (int tb = 0; tb < TB; tb++) fr[set][tb] = *(const v4i *)(sact(slot) + tb * 1024 + vfr);
     };
     auto read_weights = [&](int slot) __attribute__((always_inline)) {
 #pragma unroll
@@ -146,8 +156,8 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmA
         for (int ob = 0; ob < 4; ob++) bw[set][ob] = widen_trits(rw[ob]);
     };
 
-    v4i acc[8][4];
-    float accf[8][4][4];
+    v4i acc[TB][4];
+    float accf[TB][4][4];
 
     // one K step of the current tile. SLOT = i % 8; H = i % 2 (0: the group's first step, 1: its second);
     // FIRST: group 0 (the fp32 fold starts from zero); NEXT: this step's loads are the next tile's step i+6-nk
@@ -157,15 +167,15 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmA
         constexpr int q = SLOT >> 1;                          // group slot of this step (i % 8 == SLOT)
         constexpr int qn = ((SLOT + kPDg) >> 1) & 3;          // group slot of the step whose loads issue now
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(kWaitG));
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(wait_g(TB)));
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         // LDS reads that this step's VALU work waits for
-        float xsv[8];
+        float xsv[TB];
         float4 wsv[4];
         if constexpr (H == 1) {
 #pragma unroll
-            for (int tb = 0; tb < 8; tb++) xsv[tb] = sxs(q)[tb * 16 + l16];
+            for (int tb = 0; tb < TB; tb++) xsv[tb] = sxs(q)[tb * 16 + l16];
 #pragma unroll
             for (int ob = 0; ob < 4; ob++) wsv[ob] = *(const float4 *)&sws(q)[wave * 64 + ob * 16 + lq * 4];
         }
@@ -189,7 +199,7 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmA
                 accf[tb][ob][e] = __builtin_fmaf((float)acc[tb][ob][e], p, FIRST ? 0.0f : accf[tb][ob][e]);
             }
         };
-        static_for<0, 32>([&](auto B) __attribute__((always_inline)) {
+        static_for<0, 4 * TB>([&](auto B) __attribute__((always_inline)) {
             constexpr int b = decltype(B)::value, tb = b >> 2, ob = b & 3;
             if constexpr (H == 0) {
                 acc[tb][ob] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[fs][ob], fr[fs][tb], v4i{0, 0, 0, 0}, 0, 0, 0);
@@ -198,7 +208,10 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmA
                 if constexpr (b >= 4) fold((b - 4) >> 2, (b - 4) & 3);
             }
         });
-        if constexpr (H == 1) static_for<28, 32>([&](auto B) __attribute__((always_inline)) { fold(decltype(B)::value >> 2, decltype(B)::value & 3); });
+        if constexpr (H == 1)
+            static_for<4 * TB - 4, 4 * TB>([&](auto B) __attribute__((always_inline)) {
+                fold(decltype(B)::value >> 2, decltype(B)::value & 3);
+            });
         widen(fs ^ 1);
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -214,7 +227,7 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmA
                 b4 = __builtin_amdgcn_raw_buffer_load_b128(brs, (uint32_t)(n0 + wave * 64 + ob * 16 + lq * 4) * 4, 0,
                                                            0);
 #pragma unroll
-            for (int tb = 0; tb < 8; tb++) {
+            for (int tb = 0; tb < TB; tb++) {
                 const uint32_t so = sy + (uint32_t)(tb * 16) * out4 + (uint32_t)(ob * 64);
                 v4i old = v4i{0, 0, 0, 0};
                 if constexpr (EP == VX_EP_ADD_SCALED) old = __builtin_amdgcn_raw_buffer_load_b128(yrs, vyl, so, 0);
@@ -228,7 +241,7 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmA
                     if constexpr (BIAS) res = res + __int_as_float(b4[e]);
                     r[e] = __float_as_int(res);
                 }
-                __builtin_amdgcn_raw_buffer_store_b128(r, yrs, vyl, so, 0);
+                store_b128_sep(r, yrs, vyl, so);
             }
         }
     };
@@ -239,7 +252,7 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmA
         loads(i, (i >> 1) & 3, i & 1, i, true, vdma, sa_cur, vwd, sw_cur, m0, n0);
         __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 * (kPDg - 1)));  // the loads of step 0 complete
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(vmem_per_step(TB) * (kPDg - 1)));  // the loads of step 0 complete
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     read_frags(0, 0);
@@ -276,12 +289,22 @@ __global__ __launch_bounds__(256, 1) void tgemm_stream_groups_kernel(const GemmA
     __builtin_amdgcn_s_waitcnt(0);
 }
 
-template <int EP>
+template <int EP, int TB>
 void launch_groups(const GemmArgs &a, const StreamGeom &g, int grid, bool bias, hipStream_t st) {
     if (bias)
-        tgemm_stream_groups_kernel<EP, true><<<grid, 256, 0, st>>>(a, g);
+        tgemm_stream_groups_kernel<EP, true, TB><<<grid, 256, 0, st>>>(a, g);
     else
-        tgemm_stream_groups_kernel<EP, false><<<grid, 256, 0, st>>>(a, g);
+        tgemm_stream_groups_kernel<EP, false, TB><<<grid, 256, 0, st>>>(a, g);
+}
+
+template <int TB>
+void launch_groups_ep(const GemmArgs &a, const StreamGeom &g, int grid, bool bias, hipStream_t st) {
+    if (a.ep == VX_EP_SILU)
+        launch_groups<VX_EP_SILU, TB>(a, g, grid, bias, st);
+    else if (a.ep == VX_EP_ADD_SCALED)
+        launch_groups<VX_EP_ADD_SCALED, TB>(a, g, grid, bias, st);
+    else
+        launch_groups<VX_EP_STORE, TB>(a, g, grid, bias, st);
 }
 
 }  // namespace
@@ -293,27 +316,31 @@ bool gemm_stream_groups(const GemmArgs &a, int tokens_full, hipStream_t st) {
     if (a.out % kBN != 0 || a.r0 != 0 || a.r1 != a.out || a.t0 != 0 || tokens_full % kBM != 0) return false;
     const int forced = overrides().gemm.load(std::memory_order_relaxed);
     if (forced != kForceNone && forced != kForceStream) return false;
+    // 64-token tiles with two workgroups per CU (at 8192 tokens: FFN-up 76 -> 65 us, FFN-down 64 -> 53 us against
+    // 128-token tiles with one), or 128-token tiles ("stream_tile" override: 4 or 8 token blocks per wavefront)
+    int tb = 4;
+    const int ft = overrides().stream_tb.load(std::memory_order_relaxed);
+    if (ft == 4 || ft == 8) tb = ft;
+    const int bm = 16 * tb;
     StreamGeom g;
     g.n_nt = (int)(a.out / kBN);
-    g.ntiles = (tokens_full / kBM) * g.n_nt;
+    g.ntiles = (tokens_full / bm) * g.n_nt;
     g.per_xcd = (g.ntiles + 7) / 8;
     g.nk = (int)nk;
     g.ng = (int)a.ng;
-    const int cus = cu_count();
-    if (g.ntiles < cus / 2 && forced == kForceNone) return false;  // too few tiles: the other kernels
-    int per_x = std::min(cus / 8, g.per_xcd);
+    const int cus = cu_count(), wpc = tb == 4 ? 2 : 1;  // workgroups per CU
+    if ((tokens_full / kBM) * g.n_nt < cus / 2 && forced == kForceNone) return false;  // too few tiles
+    int per_x = std::min(wpc * cus / 8, g.per_xcd);
     const int fg = overrides().stream_grid.load(std::memory_order_relaxed);  // workgroups: tests and tuning
     if (fg >= 8) per_x = std::min(fg / 8, g.per_xcd);
     const int grid = 8 * per_x;
     GemmArgs b = a;
     b.t1 = tokens_full;
     const bool bias = a.bias != nullptr;
-    if (a.ep == VX_EP_SILU)
-        launch_groups<VX_EP_SILU>(b, g, grid, bias, st);
-    else if (a.ep == VX_EP_ADD_SCALED)
-        launch_groups<VX_EP_ADD_SCALED>(b, g, grid, bias, st);
+    if (tb == 4)
+        launch_groups_ep<4>(b, g, grid, bias, st);
     else
-        launch_groups<VX_EP_STORE>(b, g, grid, bias, st);
+        launch_groups_ep<8>(b, g, grid, bias, st);
     hip_check(hipGetLastError(), "tgemm_stream_groups launch");
     return true;
 }

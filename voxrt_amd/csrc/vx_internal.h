@@ -54,6 +54,27 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
 
+// A 16-byte buffer store whose data registers are not written again by the next instructions: two wait states
+// (s_nop 1) pinned right after it. A VMEM store of more than 8 bytes may read its data registers after it issues;
+// with the VALU write of one of them right behind the store (which the compiler emits), the store can send the new
+// value when the memory pipeline is busy (seen with two streaming workgroups per CU: the fourth dword of stored
+// outputs replaced by the next output's intermediate).
+__device__ inline void store_b128_sep(v4i v, __amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, soff, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 1");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The same separation for a 16-byte global store through a plain pointer (float4, uint4).
+template <typename T> __device__ inline void store16_sep(T *p, T v) {
+    static_assert(sizeof(T) == 16, "16-byte stores only");
+    *p = v;
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 1");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 __device__ inline float bits_f32(uint32_t u) { return __uint_as_float(u); }
 
 // Note: reinterpret an element of an ext_vector_type through __int_as_float(v[e]), never

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void quantize_fast_kernel(const float *__restr
                     w[i] = (uint32_t)(uint8_t)c0_ | ((uint32_t)(uint8_t)c1 << 8) | ((uint32_t)(uint8_t)c2 << 16) |
                            ((uint32_t)(uint8_t)c3 << 24);
                 }
-                *(uint4 *)(qr + base) = make_uint4(w[0], w[1], w[2], w[3]);
+                store16_sep((uint4 *)(qr + base), make_uint4(w[0], w[1], w[2], w[3]));
             }
         }
 #pragma unroll
@@ -268,8 +268,8 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
         for (int c = 0; c < NC; c++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                *(float4 *)(yr + c * 1024 + lane * 16 + 4 * i) =
-                    make_float4(v[c][4 * i], v[c][4 * i + 1], v[c][4 * i + 2], v[c][4 * i + 3]);
+                store16_sep((float4 *)(yr + c * 1024 + lane * 16 + 4 * i),
+                            make_float4(v[c][4 * i], v[c][4 * i + 1], v[c][4 * i + 2], v[c][4 * i + 3]));
         if constexpr (MODE == 1) return;
     }
     if constexpr (MODE == 2) ln_pass(lgv2, lbv2);
@@ -297,7 +297,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
                 wd[i] = (uint32_t)(uint8_t)c0 | ((uint32_t)(uint8_t)c1 << 8) | ((uint32_t)(uint8_t)c2 << 16) |
                         ((uint32_t)(uint8_t)c3 << 24);
             }
-            *(uint4 *)(qr + c * 1024 + lane * 16) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+            store16_sep((uint4 *)(qr + c * 1024 + lane * 16), make_uint4(wd[0], wd[1], wd[2], wd[3]));
 #pragma unroll
             for (int o = 1; o < L; o <<= 1) sum += __shfl_xor(sum, o, 64);
             if ((lane & (L - 1)) == 0) {
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
                     wd[i] = (uint32_t)(uint8_t)a0 | ((uint32_t)(uint8_t)a1 << 8) | ((uint32_t)(uint8_t)a2 << 16) |
                             ((uint32_t)(uint8_t)a3 << 24);
                 }
-                *(uint4 *)(qr + c * 1024 + lane * 16) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+                store16_sep((uint4 *)(qr + c * 1024 + lane * 16), make_uint4(wd[0], wd[1], wd[2], wd[3]));
             }
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
