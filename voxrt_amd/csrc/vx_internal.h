@@ -77,6 +77,42 @@ template <typename T> __device__ inline void store16_sep(T *p, T v) {
 
 __device__ inline float bits_f32(uint32_t u) { return __uint_as_float(u); }
 
+// Butterfly reduction over aligned groups of L lanes (L a power of two up to 64; every lane of the wavefront
+// active), for order-independent operations only (max, integer sums). Distances 1 and 2 are DPP quad permutations;
+// distance 4 and 8 are the half-row and row mirrors: once every lane of an aligned d-group holds the group's value,
+// the mirror pairs each lane with a lane of the other d-group of its 2d-group. 16 and 32 go through ds_bpermute.
+template <int L, typename Op> __device__ inline int lane_group_reduce(int v, Op op) {
+    static_assert(L >= 1 && L <= 64 && (L & (L - 1)) == 0, "L must be a power of two up to 64");
+    if constexpr (L > 1) v = op(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    if constexpr (L > 2) v = op(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    if constexpr (L > 4) v = op(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    if constexpr (L > 8) v = op(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false));  // row_mirror
+    if constexpr (L > 16) v = op(v, __shfl_xor(v, 16, 64));
+    if constexpr (L > 32) v = op(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+template <int L> __device__ inline int lane_group_sum(int v) {
+    return lane_group_reduce<L>(v, [](int a, int b) { return a + b; });
+}
+
+// max of non-negative floats (amax of |x|): compared as floats, so the result is the float max of the group
+template <int L> __device__ inline float lane_group_max(float m) {
+    return __int_as_float(lane_group_reduce<L>(__float_as_int(m), [](int a, int b) {
+        return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
+    }));
+}
+
+// The reference's hsum4 of eight running sums held in lanes 0-7: (s0+s4 + s1+s5) + (s2+s6 + s3+s7), read out with
+// v_readlane so the result is uniform across the wavefront.
+__device__ inline float hsum8_lanes(float s) {
+    float a[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) a[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), j));
+    const float p0 = a[0] + a[4], p1 = a[1] + a[5], p2 = a[2] + a[6], p3 = a[3] + a[7];
+    return (p0 + p1) + (p2 + p3);
+}
+
 // Note: reinterpret an element of an ext_vector_type through __int_as_float(v[e]), never
 // __builtin_bit_cast(float, v[e]): this clang lowers the latter to element 0 whatever e is.
 

@@ -211,43 +211,48 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's row is in LDS
         __builtin_amdgcn_wave_barrier();
         float mean, linv;
-        // lane j < 8 keeps the running sum of columns j, j+8, j+16, ... in that order
+        // lane j < 8 keeps the running sum of columns j, j+8, j+16, ... in that order. Each 128-value stretch of
+        // its column is read from LDS in one batch before the dependent additions start.
         float s = 0.0f;
         if (lane < 8) {
             const float *r = T + lane * KL;
-#pragma unroll 4
-            for (int k = 0; k < KL; k += 4) {
-                const float4 f = *(const float4 *)(r + k);
-                s += f.x;
-                s += f.y;
-                s += f.z;
-                s += f.w;
+#pragma unroll
+            for (int k0 = 0; k0 < KL; k0 += 128) {
+                float4 f[32];
+#pragma unroll
+                for (int k = 0; k < 32; k++) f[k] = *(const float4 *)(r + k0 + 4 * k);
+#pragma unroll
+                for (int k = 0; k < 32; k++) {
+                    s += f[k].x;
+                    s += f[k].y;
+                    s += f[k].z;
+                    s += f[k].w;
+                }
             }
         }
-        float pr = s + __shfl(s, lane + 4, 64);
-        float sum = (pr + __shfl(pr, 1, 64)) + (__shfl(pr, 2, 64) + __shfl(pr, 3, 64));
-        sum = __shfl(sum, 0, 64);
-        mean = sum / (float)inp;
+        mean = hsum8_lanes(s) / (float)inp;
         float qs = 0.0f;
         if (lane < 8) {
             const float *r = T + lane * KL;
-#pragma unroll 4
-            for (int k = 0; k < KL; k += 4) {
-                const float4 f = *(const float4 *)(r + k);
-                float a = f.x - mean;
-                qs = __builtin_fmaf(a, a, qs);
-                a = f.y - mean;
-                qs = __builtin_fmaf(a, a, qs);
-                a = f.z - mean;
-                qs = __builtin_fmaf(a, a, qs);
-                a = f.w - mean;
-                qs = __builtin_fmaf(a, a, qs);
+#pragma unroll
+            for (int k0 = 0; k0 < KL; k0 += 128) {
+                float4 f[32];
+#pragma unroll
+                for (int k = 0; k < 32; k++) f[k] = *(const float4 *)(r + k0 + 4 * k);
+#pragma unroll
+                for (int k = 0; k < 32; k++) {
+                    float a = f[k].x - mean;
+                    qs = __builtin_fmaf(a, a, qs);
+                    a = f[k].y - mean;
+                    qs = __builtin_fmaf(a, a, qs);
+                    a = f[k].z - mean;
+                    qs = __builtin_fmaf(a, a, qs);
+                    a = f[k].w - mean;
+                    qs = __builtin_fmaf(a, a, qs);
+                }
             }
         }
-        pr = qs + __shfl(qs, lane + 4, 64);
-        float sq = (pr + __shfl(pr, 1, 64)) + (__shfl(pr, 2, 64) + __shfl(pr, 3, 64));
-        sq = __shfl(sq, 0, 64);
-        const float var = sq / (float)inp;
+        const float var = hsum8_lanes(qs) / (float)inp;
         linv = 1.0f / __builtin_sqrtf(var + 1e-5f);
 #pragma unroll
         for (int c = 0; c < NC; c++) {
@@ -283,8 +288,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
             float m = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[c][i]));
-#pragma unroll
-            for (int o = 1; o < L; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            m = lane_group_max<L>(m);
             const float sc = m == 0.0f ? 1.0f : m / 127.0f;
             const float inv = 1.0f / sc;
             int sum = 0;
@@ -298,8 +302,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
                         ((uint32_t)(uint8_t)c3 << 24);
             }
             store16_sep((uint4 *)(qr + c * 1024 + lane * 16), make_uint4(wd[0], wd[1], wd[2], wd[3]));
-#pragma unroll
-            for (int o = 1; o < L; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            sum = lane_group_sum<L>(sum);
             if ((lane & (L - 1)) == 0) {
                 const int g = (c * 1024 + lane * 16) / group;
                 st[(int64_t)g * np + t] = sc;
@@ -316,9 +319,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
                 if (c >= c0 && c < c0 + cpg)
 #pragma unroll
                     for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[c][i]));
-            m = fmaxf(m, 0.0f);
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            m = lane_group_max<64>(fmaxf(m, 0.0f));
             const float sc = m == 0.0f ? 1.0f : m / 127.0f;
             const float inv = 1.0f / sc;
             int sum = 0;
@@ -336,8 +337,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
                 }
                 store16_sep((uint4 *)(qr + c * 1024 + lane * 16), make_uint4(wd[0], wd[1], wd[2], wd[3]));
             }
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            sum = lane_group_sum<64>(sum);
             if (lane == 0) {
                 const int g = c0 / cpg;
                 st[(int64_t)g * np + t] = sc;
