@@ -15,10 +15,11 @@
 //   attn_prep_kernel  : the row items (one wavefront per 128-wide row: q+bias_u, q+bias_v, k (tokens), relative
 //                       rows; quantize) and the vT items (one wavefront per (head, channel): the column of v over
 //                       the tokens, quantized) in one launch.
-//   attn_core_kernel  : one workgroup per (head, 16 query rows). Content scores for all keys and the position band
-//                       [t-1-i_max, 2t-2-i0] through v_mfma_i32_16x16x64_i8 into LDS; softmax in LDS (the four
-//                       running sums per row on four lanes, so the order is the reference's); the probabilities
-//                       quantized into LDS; P . vT through the same MFMA; ctx written in place in [t][d].
+//   attn_core_kernel  : one workgroup per (head, 16 query rows). Content scores for all keys through
+//                       v_mfma_i32_16x16x64_i8 into LDS, the position band [t-1-i_max, 2t-2-i0] through the same MFMA
+//                       added to them in place; softmax in LDS (the four running sums per row on four lanes, so the
+//                       order is the reference's); the probabilities quantized into LDS; P . vT through the same
+//                       MFMA; ctx written in place in [t][d].
 #include <atomic>
 #include <string>
 
@@ -167,15 +168,13 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const float *__restrict_
         attn_vt_item(((int)blockIdx.x - rows_blocks) * 4 + wv, qkv, D, W);
 }
 
-// LDS plan of attn_core_kernel (bytes): s1 [16][s1w] f32, s2 [16][s2w] f32, pq [16][tv] int8, row stats (kRowv
-// words: [0,16) max, [16,32) 1/sum, [32,48) probability scale, [64,192) and [192,320) the quantized output's
-// per-wavefront row maxima and code sums).
+// LDS plan of attn_core_kernel (bytes): scores [16][s1w] f32 (content scores, then the band added in place, then the
+// exponentials), pq [16][tv] int8, row stats (kRowv words: [0,16) max, [16,32) 1/sum, [32,48) probability scale,
+// [64,192) and [192,320) the quantized output's per-wavefront row maxima and code sums).
 constexpr int kCoreWaves = 8, kRowv = 320;
 __host__ __device__ inline int s1w_of(int t) { return up16(t) + 4; }
-// the band of a block spans at most t + 45 positions after its start is rounded down to a 16-block
-__host__ __device__ inline int s2w_of(int t) { return up16(t + 48) + 4; }
 __host__ __device__ inline size_t core_lds_bytes(int t) {
-    return (size_t)16 * s1w_of(t) * 4 + (size_t)16 * s2w_of(t) * 4 + (size_t)16 * up64(t) + kRowv * 4;
+    return (size_t)16 * s1w_of(t) * 4 + (size_t)16 * up64(t) + kRowv * 4;
 }
 
 // ctx written as the o-projection's int8 activations (Attention::forward_fused, encoder.rs:180-183: attn_core_int8
@@ -188,16 +187,17 @@ struct AttnQOut {
     int np;        // npad(nseg * t)
 };
 
-// Eight wavefronts: the key and band blocks are dealt out over them, each query row's softmax runs on 32 lanes, and
-// each wavefront owns one 16-channel block of the context.
+// Eight wavefronts: the key and band blocks are dealt out over them, each query row's softmax runs on 32 lanes (four
+// consecutive columns per lane), and each wavefront owns one 16-channel block of the context. Every global operand
+// is requested before the phase that needs it starts: the band rows with the keys, the vT rows of the context
+// product right after the content scores.
 template <bool QOUT>
-__global__ __launch_bounds__(64 * kCoreWaves) void attn_core_kernel(AttnDims D, AttnWs W, float scaling,
-                                                                    float *__restrict__ ctx, AttnQOut Q) {
+__global__ __launch_bounds__(64 * kCoreWaves, 2) void attn_core_kernel(AttnDims D, AttnWs W, float scaling,
+                                                                       float *__restrict__ ctx, AttnQOut Q) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int s1w = s1w_of(D.t), s2w = s2w_of(D.t);
+    const int s1w = s1w_of(D.t);
     float *s1 = (float *)smem;
-    float *s2 = s1 + 16 * s1w;
-    int8_t *pq = (int8_t *)(s2 + 16 * s2w);
+    int8_t *pq = (int8_t *)(s1 + 16 * s1w);
     float *rowv = (float *)(pq + 16 * D.tv);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.y, i0 = blockIdx.x * 16;
@@ -217,6 +217,7 @@ __global__ __launch_bounds__(64 * kCoreWaves) void attn_core_kernel(AttnDims D, 
     }
     const int64_t row0 = (int64_t)blockIdx.z * D.t;  // this segment's first token row
     const int imax = min(i0 + 15, t - 1);
+    const int nrows = imax - i0 + 1;             // valid query rows of the block
     const int pb0 = (t - 1 - imax) & ~15;        // first position block of the band
     const int pend = 2 * t - 2 - i0;             // last position used by the block
     const int npb = (pend - pb0) / 16 + 1;       // position blocks
@@ -236,9 +237,23 @@ __global__ __launch_bounds__(64 * kCoreWaves) void attn_core_kernel(AttnDims D, 
         qus[e] = W.qus[h * D.tp + i0 + drow + e];
         qvs[e] = W.qvs[h * D.tp + i0 + drow + e];
     }
+    constexpr int kPF = 4, NW = kCoreWaves;
+    // band operands of kPF of this wave's position blocks q0, q0+8, ... (past the last block: a repeat of it)
+    v4i r0[kPF], r1[kPF];
+    float rsv[kPF];
+    auto load_band = [&](int q0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < kPF; p++) {
+            const int p0 = pb0 + min(q0 + NW * p, npb - 1) * 16;
+            const int8_t *rr = W.rq + ((int64_t)h * D.rp + p0 + arow) * kDh + 16 * aq;
+            r0[p] = *(const v4i *)rr;
+            r1[p] = *(const v4i *)(rr + 64);
+            rsv[p] = W.rs[h * D.rp + p0 + dcol];
+        }
+    };
+    load_band(wave);
     // content scores: key block kb -> s1[row][16*kb + col]. A wave takes blocks wave, wave+8, ...; the loads of
     // kPF of its blocks are issued before their MFMAs (past the last block: a repeat of it, not used)
-    constexpr int kPF = 4, NW = kCoreWaves;
     for (int kb0 = wave; kb0 < nkb; kb0 += NW * kPF) {
         v4i b0[kPF], b1[kPF];
         float ksv[kPF];
@@ -263,50 +278,59 @@ __global__ __launch_bounds__(64 * kCoreWaves) void attn_core_kernel(AttnDims D, 
             }
         }
     }
-    // position band: block pb -> s2[row][16*pb' + col], position pb0 + 16*pb' + col (loads ahead as above)
-    for (int q0 = wave; q0 < npb; q0 += NW * kPF) {
-        v4i b0[kPF], b1[kPF];
-        float rsv[kPF];
+    // the context product's vT operands (channel block `wave`, the first kVPre K steps of 64 tokens)
+    constexpr int kVPre = 6;
+    const int8_t *vr0 = W.vq + ((int64_t)h * kDh + wave * 16 + arow) * D.tv + 16 * aq;
+    v4i vb[kVPre];
 #pragma unroll
-        for (int p = 0; p < kPF; p++) {
-            const int p0 = pb0 + min(q0 + NW * p, npb - 1) * 16;
-            const int8_t *rr = W.rq + ((int64_t)h * D.rp + p0 + arow) * kDh + 16 * aq;
-            b0[p] = *(const v4i *)rr;
-            b1[p] = *(const v4i *)(rr + 64);
-            rsv[p] = W.rs[h * D.rp + p0 + dcol];
-        }
+    for (int p = 0; p < kVPre; p++) vb[p] = *(const v4i *)(vr0 + min(64 * p, D.tv - 64));
+    __syncthreads();  // s1 holds the content scores
+    // position band: block pb, column col is position p = pb0 + 16*pb + col, i.e. key j = p - (t-1-i) of query
+    // row i; score = S1 + S2 is formed in place (each (row, key) of the block is one (block, column) of the band)
+    for (int q0 = wave; q0 < npb; q0 += NW * kPF) {
+        if (q0 != wave) load_band(q0);
 #pragma unroll
         for (int p = 0; p < kPF; p++) {
             const int pb = q0 + NW * p;
             if (pb < npb) {
                 v4i acc = {0, 0, 0, 0};
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0[p], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1[p], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, r0[p], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, r1[p], acc, 0, 0, 0);
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    s2[(drow + e) * s2w + pb * 16 + dcol] = __builtin_fmaf((float)acc[e], qvs[e] * rsv[p], 0.0f);
+                for (int e = 0; e < 4; e++) {
+                    const int r = drow + e;
+                    const int j = pb0 + pb * 16 + dcol - (t - 1 - (i0 + r));
+                    if (r < nrows && j >= 0 && j < t)
+                        s1[r * s1w + j] = s1[r * s1w + j] + __builtin_fmaf((float)acc[e], qvs[e] * rsv[p], 0.0f);
+                }
             }
         }
     }
     __syncthreads();
-    const int nrows = imax - i0 + 1;  // valid query rows of the block
-    // per row (32 lanes, wave w rows 2w, 2w+1): score = S1 + S2[t-1-i+j] in place in s1, the row max of
+    // per row (32 lanes, wave w rows 2w, 2w+1; lane l32 columns 4*l32 + 128*k .. +3): the row max of
     // score * scaling, then exp_poly(score * scaling - max) in place
     {
         const int r = wave * 2 + (lane >> 5), l32 = lane & 31;
+        float *sr = s1 + r * s1w;
         float m = -INFINITY;
-        if (r < nrows) {
-            const float *s2r = s2 + r * s2w + (t - 1 - (i0 + r) - pb0);
-            for (int j = l32; j < t; j += 32) {
-                const float sc = s1[r * s1w + j] + s2r[j];
-                s1[r * s1w + j] = sc;
-                m = fmaxf(m, sc * scaling);
-            }
-        }
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
         if (r < nrows)
-            for (int j = l32; j < t; j += 32) s1[r * s1w + j] = exp_poly(s1[r * s1w + j] * scaling - m);
+            for (int j = 4 * l32; j < t; j += 128) {
+                const float4 f = *(const float4 *)(sr + j);
+                m = fmaxf(m, f.x * scaling);
+                if (j + 1 < t) m = fmaxf(m, f.y * scaling);
+                if (j + 2 < t) m = fmaxf(m, f.z * scaling);
+                if (j + 3 < t) m = fmaxf(m, f.w * scaling);
+            }
+        m = lane_group_max<32>(m);
+        if (r < nrows)
+            for (int j = 4 * l32; j < t; j += 128) {
+                float4 f = *(const float4 *)(sr + j);
+                f.x = exp_poly(f.x * scaling - m);
+                f.y = exp_poly(f.y * scaling - m);
+                f.z = exp_poly(f.z * scaling - m);
+                f.w = exp_poly(f.w * scaling - m);
+                *(float4 *)(sr + j) = f;  // columns past t (inside the row's pitch) are never read as scores
+            }
     }
     __syncthreads();
     // row sums in the reference's order: lane 4r + l keeps the running sum of columns j = 4q + l
@@ -326,30 +350,48 @@ __global__ __launch_bounds__(64 * kCoreWaves) void attn_core_kernel(AttnDims D, 
             for (int j = t4; j < t; j++) sum += s1[r * s1w + j];
         if (l == 0) rowv[16 + r] = 1.0f / sum;
     }
-    // probability quantization: amax per row (32 lanes per row), codes into pq, zero to tv
+    // probability quantization: amax per row (32 lanes per row), four codes per lane and step into pq, zero to tv
     {
         const int r = wave * 2 + (lane >> 5), l32 = lane & 31;
+        const float *sr = s1 + r * s1w;
         float m = 0.0f;
         if (r < nrows)
-            for (int j = l32; j < t; j += 32) m = fmaxf(m, fabsf(s1[r * s1w + j]));
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            for (int j = 4 * l32; j < t; j += 128) {
+                const float4 f = *(const float4 *)(sr + j);
+                m = fmaxf(m, fabsf(f.x));
+                if (j + 1 < t) m = fmaxf(m, fabsf(f.y));
+                if (j + 2 < t) m = fmaxf(m, fabsf(f.z));
+                if (j + 3 < t) m = fmaxf(m, fabsf(f.w));
+            }
+        m = lane_group_max<32>(m);
         const float s = m == 0.0f ? 1.0f : m / 127.0f;
         const float inv = 1.0f / s;
-        for (int j = l32; j < D.tv; j += 32)
-            pq[r * D.tv + j] = (r < nrows && j < t) ? q_code(s1[r * s1w + j], inv) : (int8_t)0;
+        for (int j = 4 * l32; j < D.tv; j += 128) {
+            uint32_t w4 = 0;
+            if (r < nrows && j < t) {
+                const float4 f = *(const float4 *)(sr + j);
+                const uint32_t c0 = (uint8_t)q_code(f.x, inv);
+                const uint32_t c1 = j + 1 < t ? (uint8_t)q_code(f.y, inv) : 0u;
+                const uint32_t c2 = j + 2 < t ? (uint8_t)q_code(f.z, inv) : 0u;
+                const uint32_t c3 = j + 3 < t ? (uint8_t)q_code(f.w, inv) : 0u;
+                w4 = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+            }
+            *(uint32_t *)(pq + r * D.tv + j) = w4;
+        }
         __syncthreads();  // the 1/sum of wave 0 is visible after this barrier
         if (l32 == 0) rowv[32 + r] = s * rowv[16 + r];
     }
     __syncthreads();
-    // context: channel block `wave`; K over tv in 64-steps; A = pq rows from LDS, B = vT rows (the vT loads of
-    // kPF K steps are issued before their MFMAs)
+    // context: channel block `wave`; K over tv in 64-steps; A = pq rows from LDS, B = vT rows (the first kVPre
+    // steps loaded above, the loads of kPF later steps issued before their MFMAs)
     float val[4];
     v4i pacc = {0, 0, 0, 0};
     {
-        const int8_t *vr0 = W.vq + ((int64_t)h * kDh + wave * 16 + arow) * D.tv + 16 * aq;
         const int8_t *pr = pq + arow * D.tv + 16 * aq;
-        for (int k0 = 0; k0 < D.tv; k0 += 64 * kPF) {
+#pragma unroll
+        for (int p = 0; p < kVPre; p++)
+            if (64 * p < D.tv) pacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i *)(pr + 64 * p), vb[p], pacc, 0, 0, 0);
+        for (int k0 = 64 * kVPre; k0 < D.tv; k0 += 64 * kPF) {
             v4i b[kPF];
 #pragma unroll
             for (int p = 0; p < kPF; p++) b[p] = *(const v4i *)(vr0 + min(k0 + 64 * p, D.tv - 64));
@@ -379,9 +421,7 @@ __global__ __launch_bounds__(64 * kCoreWaves) void attn_core_kernel(AttnDims D, 
         float sc[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            float m = fabsf(val[e]);
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            const float m = lane_group_max<16>(fabsf(val[e]));
             if (dcol == 0) qmax[wave * 16 + drow + e] = m;
         }
         __syncthreads();
@@ -395,9 +435,7 @@ __global__ __launch_bounds__(64 * kCoreWaves) void attn_core_kernel(AttnDims D, 
             const float inv = 1.0f / sc[e];
             const int8_t c0 = q_code(val[e], inv);
             if (r < nrows) Q.q[(row0 + i0 + r) * D.d + h * kDh + wave * 16 + dcol] = c0;
-            int sum = (int)c0;
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            const int sum = lane_group_sum<16>((int)c0);
             if (dcol == 0) qsum[wave * 16 + r] = sum;
         }
         __syncthreads();
