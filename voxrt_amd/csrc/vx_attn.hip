@@ -161,11 +161,21 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const float *__restrict_
                                                        const float *__restrict__ bias_u,
                                                        const float *__restrict__ bias_v, AttnDims D, AttnWs W,
                                                        int rows_blocks) {
-    const int wv = threadIdx.x >> 6;
-    if ((int)blockIdx.x < rows_blocks)
-        attn_rows_item((int)blockIdx.x * 4 + wv, qkv, rel_k, bias_u, bias_v, D, W);
-    else
-        attn_vt_item(((int)blockIdx.x - rows_blocks) * 4 + wv, qkv, D, W);
+    // Head-major workgroups go to the XCD of their head (workgroup b runs on XCD b % 8, the core's workgroups of head
+    // h on XCD h % 8 with eight heads): the token rows of (segment, head) are tp/4 workgroups b with b % h == head,
+    // the relative rows (when quantized here) follow in order, the vT rows start at rows_blocks (a multiple of 64)
+    // with the same head rule.
+    const int wv = threadIdx.x >> 6, b = blockIdx.x;
+    const int tok_blocks = D.nseg * D.h * (D.tp / 4);
+    if (b < tok_blocks) {
+        const int head = b % D.h, rest = b / D.h, seg = rest / (D.tp / 4), chunk = rest % (D.tp / 4);
+        attn_rows_item(((seg * D.h + head) * D.tp) + chunk * 4 + wv, qkv, rel_k, bias_u, bias_v, D, W);
+    } else if (b < rows_blocks) {
+        attn_rows_item(b * 4 + wv, qkv, rel_k, bias_u, bias_v, D, W);  // relative rows (and padding)
+    } else {
+        const int v = b - rows_blocks, head = v % D.h, rest = v / D.h, seg = rest / (kDh / 4), chunk = rest % (kDh / 4);
+        attn_vt_item((seg * D.h + head) * kDh + chunk * 4 + wv, qkv, D, W);
+    }
 }
 
 // LDS plan of attn_core_kernel (bytes): scores [16][s1w] f32 (content scores, then the band added in place, then the
@@ -190,8 +200,11 @@ struct AttnQOut {
 // Eight wavefronts: the key and band blocks are dealt out over them, each query row's softmax runs on 32 lanes (four
 // consecutive columns per lane), and each wavefront owns one 16-channel block of the context. Every global operand
 // is requested before the phase that needs it starts: the band rows with the keys, the vT rows of the context
-// product right after the content scores.
-template <bool QOUT>
+// product right after the content scores. The workgroup's vector-memory instructions are few because each costs the
+// address unit 16 cycles whatever its width: KPF (the blocks a wave takes per batch) is the smallest depth that
+// covers the keys and the band in one batch (up to 4; loops take the rest), the query scales are one 16-byte load,
+// and one load per batch brings the scales of all its blocks, handed to the lanes that use them by ds_bpermute.
+template <bool QOUT, int KPF>
 __global__ __launch_bounds__(64 * kCoreWaves, 2) void attn_core_kernel(AttnDims D, AttnWs W, float scaling,
                                                                        float *__restrict__ ctx, AttnQOut Q) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -199,8 +212,12 @@ __global__ __launch_bounds__(64 * kCoreWaves, 2) void attn_core_kernel(AttnDims 
     float *s1 = (float *)smem;
     int8_t *pq = (int8_t *)(s1 + 16 * s1w);
     float *rowv = (float *)(pq + 16 * D.tv);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int h = blockIdx.y, i0 = blockIdx.x * 16;
+    // wave is uniform across the wavefront; readfirstlane lets the compiler know it, so the loops over a wave's
+    // blocks are scalar loops and the loads issued ahead of them are not drained at their heads
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // workgroup id = query block * h + head: with eight heads one head's workgroups run on one XCD (workgroup b runs
+    // on XCD b % 8) and share its keys, band rows and vT in that XCD's L2
+    const int h = blockIdx.x % D.h, qb = blockIdx.x / D.h, i0 = qb * 16;
     const int t = D.t;
     // segment blockIdx.z: its per-token tables and its rows of ctx (the relative rows are shared)
     {
@@ -231,16 +248,32 @@ __global__ __launch_bounds__(64 * kCoreWaves, 2) void attn_core_kernel(AttnDims 
     const v4i av0 = *(const v4i *)qv, av1 = *(const v4i *)(qv + 64);
     // D element e of lane l: row 4*(l/16) + e, column l%16
     const int drow = 4 * aq, dcol = arow;
-    float qus[4], qvs[4];
+    const float4 qu4 = *(const float4 *)&W.qus[h * D.tp + i0 + drow];
+    const float4 qv4 = *(const float4 *)&W.qvs[h * D.tp + i0 + drow];
+    const float qus[4] = {qu4.x, qu4.y, qu4.z, qu4.w}, qvs[4] = {qv4.x, qv4.y, qv4.z, qv4.w};
+    constexpr int kPF = KPF, NW = kCoreWaves;
+    // Key and band operands of kPF of this wave's blocks b0, b0+8, ... (past the last block: a repeat of it, not
+    // used). The first batch of each is issued in straight-line code before any score is computed: a loop here would
+    // make the compiler drain every load issued before it (a loop that uses registers loaded ahead of it gets a full
+    // vmcnt wait at its head).
+    v4i k0v[kPF], k1v[kPF], r0[kPF], r1[kPF];
+    float ksv[kPF], rsv[kPF];
+    // lane 16p + c of a scale load holds the scale of block p's key (position) c; block p's lanes take theirs
+    auto spread = [&](float v, float (&out)[kPF]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        qus[e] = W.qus[h * D.tp + i0 + drow + e];
-        qvs[e] = W.qvs[h * D.tp + i0 + drow + e];
-    }
-    constexpr int kPF = 4, NW = kCoreWaves;
-    // band operands of kPF of this wave's position blocks q0, q0+8, ... (past the last block: a repeat of it)
-    v4i r0[kPF], r1[kPF];
-    float rsv[kPF];
+        for (int p = 0; p < kPF; p++) out[p] = __int_as_float(__shfl(__float_as_int(v), 16 * p + dcol, 64));
+    };
+    float ks_l = 0.0f, rs_l = 0.0f;  // this lane's scale of a batch (see spread)
+    auto load_keys = [&](int kb0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < kPF; p++) {
+            const int kb = min(kb0 + NW * p, nkb - 1);
+            const int8_t *kr = W.kq + ((int64_t)h * D.tp + kb * 16 + arow) * kDh + 16 * aq;
+            k0v[p] = *(const v4i *)kr;
+            k1v[p] = *(const v4i *)(kr + 64);
+        }
+        ks_l = W.ks[h * D.tp + min(kb0 + NW * min(lane >> 4, kPF - 1), nkb - 1) * 16 + dcol];
+    };
     auto load_band = [&](int q0) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < kPF; p++) {
@@ -248,47 +281,29 @@ __global__ __launch_bounds__(64 * kCoreWaves, 2) void attn_core_kernel(AttnDims 
             const int8_t *rr = W.rq + ((int64_t)h * D.rp + p0 + arow) * kDh + 16 * aq;
             r0[p] = *(const v4i *)rr;
             r1[p] = *(const v4i *)(rr + 64);
-            rsv[p] = W.rs[h * D.rp + p0 + dcol];
         }
+        rs_l = W.rs[h * D.rp + pb0 + min(q0 + NW * min(lane >> 4, kPF - 1), npb - 1) * 16 + dcol];
     };
-    load_band(wave);
-    // content scores: key block kb -> s1[row][16*kb + col]. A wave takes blocks wave, wave+8, ...; the loads of
-    // kPF of its blocks are issued before their MFMAs (past the last block: a repeat of it, not used)
-    for (int kb0 = wave; kb0 < nkb; kb0 += NW * kPF) {
-        v4i b0[kPF], b1[kPF];
-        float ksv[kPF];
-#pragma unroll
-        for (int p = 0; p < kPF; p++) {
-            const int kb = min(kb0 + NW * p, nkb - 1);
-            const int8_t *kr = W.kq + ((int64_t)h * D.tp + kb * 16 + arow) * kDh + 16 * aq;
-            b0[p] = *(const v4i *)kr;
-            b1[p] = *(const v4i *)(kr + 64);
-            ksv[p] = W.ks[h * D.tp + kb * 16 + dcol];
-        }
+    // content scores: key block kb -> s1[row][16*kb + col]
+    auto score_keys = [&](int kb0) __attribute__((always_inline)) {
+        spread(ks_l, ksv);
 #pragma unroll
         for (int p = 0; p < kPF; p++) {
             const int kb = kb0 + NW * p;
             if (kb < nkb) {
                 v4i acc = {0, 0, 0, 0};
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au0, b0[p], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au1, b1[p], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au0, k0v[p], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(au1, k1v[p], acc, 0, 0, 0);
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     s1[(drow + e) * s1w + kb * 16 + dcol] = __builtin_fmaf((float)acc[e], qus[e] * ksv[p], 0.0f);
             }
         }
-    }
-    // the context product's vT operands (channel block `wave`, the first kVPre K steps of 64 tokens)
-    constexpr int kVPre = 6;
-    const int8_t *vr0 = W.vq + ((int64_t)h * kDh + wave * 16 + arow) * D.tv + 16 * aq;
-    v4i vb[kVPre];
-#pragma unroll
-    for (int p = 0; p < kVPre; p++) vb[p] = *(const v4i *)(vr0 + min(64 * p, D.tv - 64));
-    __syncthreads();  // s1 holds the content scores
+    };
     // position band: block pb, column col is position p = pb0 + 16*pb + col, i.e. key j = p - (t-1-i) of query
     // row i; score = S1 + S2 is formed in place (each (row, key) of the block is one (block, column) of the band)
-    for (int q0 = wave; q0 < npb; q0 += NW * kPF) {
-        if (q0 != wave) load_band(q0);
+    auto score_band = [&](int q0) __attribute__((always_inline)) {
+        spread(rs_l, rsv);
 #pragma unroll
         for (int p = 0; p < kPF; p++) {
             const int pb = q0 + NW * p;
@@ -305,6 +320,25 @@ __global__ __launch_bounds__(64 * kCoreWaves, 2) void attn_core_kernel(AttnDims 
                 }
             }
         }
+    };
+    load_keys(wave);
+    load_band(wave);
+    score_keys(wave);
+    for (int kb0 = wave + NW * kPF; kb0 < nkb; kb0 += NW * kPF) {  // t > 512
+        load_keys(kb0);
+        score_keys(kb0);
+    }
+    // the context product's vT operands (channel block `wave`, the first kVPre K steps of 64 tokens)
+    constexpr int kVPre = 6;
+    const int8_t *vr0 = W.vq + ((int64_t)h * kDh + wave * 16 + arow) * D.tv + 16 * aq;
+    v4i vb[kVPre];
+#pragma unroll
+    for (int p = 0; p < kVPre; p++) vb[p] = *(const v4i *)(vr0 + min(64 * p, D.tv - 64));
+    __syncthreads();  // s1 holds the content scores
+    score_band(wave);
+    for (int q0 = wave + NW * kPF; q0 < npb; q0 += NW * kPF) {  // t > 504
+        load_band(q0);
+        score_band(q0);
     }
     __syncthreads();
     // per row (32 lanes, wave w rows 2w, 2w+1; lane l32 columns 4*l32 + 128*k .. +3): the row max of
@@ -350,36 +384,40 @@ __global__ __launch_bounds__(64 * kCoreWaves, 2) void attn_core_kernel(AttnDims 
             for (int j = t4; j < t; j++) sum += s1[r * s1w + j];
         if (l == 0) rowv[16 + r] = 1.0f / sum;
     }
-    // probability quantization: amax per row (32 lanes per row), four codes per lane and step into pq, zero to tv
+    // probability quantization on waves 4-7 while wave 0 runs the row sums: amax per row (16 lanes per row), four
+    // codes per lane and step into pq, zero to tv
     {
-        const int r = wave * 2 + (lane >> 5), l32 = lane & 31;
-        const float *sr = s1 + r * s1w;
-        float m = 0.0f;
-        if (r < nrows)
-            for (int j = 4 * l32; j < t; j += 128) {
-                const float4 f = *(const float4 *)(sr + j);
-                m = fmaxf(m, fabsf(f.x));
-                if (j + 1 < t) m = fmaxf(m, fabsf(f.y));
-                if (j + 2 < t) m = fmaxf(m, fabsf(f.z));
-                if (j + 3 < t) m = fmaxf(m, fabsf(f.w));
+        const int r = (wave - 4) * 4 + (lane >> 4), l16 = lane & 15;
+        float s = 1.0f;
+        if (wave >= 4) {
+            const float *sr = s1 + r * s1w;
+            float m = 0.0f;
+            if (r < nrows)
+                for (int j = 4 * l16; j < t; j += 64) {
+                    const float4 f = *(const float4 *)(sr + j);
+                    m = fmaxf(m, fabsf(f.x));
+                    if (j + 1 < t) m = fmaxf(m, fabsf(f.y));
+                    if (j + 2 < t) m = fmaxf(m, fabsf(f.z));
+                    if (j + 3 < t) m = fmaxf(m, fabsf(f.w));
+                }
+            m = lane_group_max<16>(m);
+            s = m == 0.0f ? 1.0f : m / 127.0f;
+            const float inv = 1.0f / s;
+            for (int j = 4 * l16; j < D.tv; j += 64) {
+                uint32_t w4 = 0;
+                if (r < nrows && j < t) {
+                    const float4 f = *(const float4 *)(sr + j);
+                    const uint32_t c0 = (uint8_t)q_code(f.x, inv);
+                    const uint32_t c1 = j + 1 < t ? (uint8_t)q_code(f.y, inv) : 0u;
+                    const uint32_t c2 = j + 2 < t ? (uint8_t)q_code(f.z, inv) : 0u;
+                    const uint32_t c3 = j + 3 < t ? (uint8_t)q_code(f.w, inv) : 0u;
+                    w4 = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+                }
+                *(uint32_t *)(pq + r * D.tv + j) = w4;
             }
-        m = lane_group_max<32>(m);
-        const float s = m == 0.0f ? 1.0f : m / 127.0f;
-        const float inv = 1.0f / s;
-        for (int j = 4 * l32; j < D.tv; j += 128) {
-            uint32_t w4 = 0;
-            if (r < nrows && j < t) {
-                const float4 f = *(const float4 *)(sr + j);
-                const uint32_t c0 = (uint8_t)q_code(f.x, inv);
-                const uint32_t c1 = j + 1 < t ? (uint8_t)q_code(f.y, inv) : 0u;
-                const uint32_t c2 = j + 2 < t ? (uint8_t)q_code(f.z, inv) : 0u;
-                const uint32_t c3 = j + 3 < t ? (uint8_t)q_code(f.w, inv) : 0u;
-                w4 = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
-            }
-            *(uint32_t *)(pq + r * D.tv + j) = w4;
         }
         __syncthreads();  // the 1/sum of wave 0 is visible after this barrier
-        if (l32 == 0) rowv[32 + r] = s * rowv[16 + r];
+        if (wave >= 4 && l16 == 0) rowv[32 + r] = s * rowv[16 + r];
     }
     __syncthreads();
     // context: channel block `wave`; K over tv in 64-steps; A = pq rows from LDS, B = vT rows (the first kVPre
@@ -454,7 +492,7 @@ __global__ __launch_bounds__(64 * kCoreWaves, 2) void attn_core_kernel(AttnDims 
             }
         }
         // pad tokens [nseg * t, np) of this head's group: zero scale and code sum
-        if (blockIdx.x == gridDim.x - 1 && blockIdx.z == gridDim.z - 1) {
+        if (qb == D.tp / 16 - 1 && blockIdx.z == gridDim.z - 1) {
             const int64_t n = (int64_t)gridDim.z * D.t;
             if (tid < Q.np - n) {
                 Q.s[(int64_t)h * Q.np + n + tid] = 0.0f;
@@ -492,12 +530,12 @@ void attention_prime() {
     hip_check(hipGetDevice(&dev), "hipGetDevice");
     const bool cached = dev >= 0 && dev < 64;
     if (cached && lds_raised[dev].load(std::memory_order_acquire)) return;
-    hip_check(hipFuncSetAttribute((const void *)attn_core_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  160 * 1024),
-              "attention LDS limit");
-    hip_check(hipFuncSetAttribute((const void *)attn_core_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  160 * 1024),
-              "attention LDS limit");
+    const void *kernels[] = {(const void *)attn_core_kernel<false, 1>, (const void *)attn_core_kernel<false, 2>,
+                             (const void *)attn_core_kernel<false, 3>, (const void *)attn_core_kernel<false, 4>,
+                             (const void *)attn_core_kernel<true, 1>,  (const void *)attn_core_kernel<true, 2>,
+                             (const void *)attn_core_kernel<true, 3>,  (const void *)attn_core_kernel<true, 4>};
+    for (const void *k : kernels)
+        hip_check(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024), "attention LDS limit");
     if (cached) lds_raised[dev].store(true, std::memory_order_release);
 }
 
@@ -543,18 +581,29 @@ void attention_core_seg(const float *qkv, const float *rel_k, int64_t nseg, int6
         W.rs = const_cast<float *>(rs_pre);
     }
     const int items = (int)(rows + (pre ? 0 : rrows));
-    const int rows_blocks = (items + 3) / 4, vt_blocks = (int)((nseg * h * kDh + 3) / 4);
+    const int rows_blocks = ((items + 3) / 4 + 63) / 64 * 64, vt_blocks = (int)((nseg * h * kDh + 3) / 4);
     attn_prep_kernel<<<(unsigned)(rows_blocks + vt_blocks), 256, 0, st>>>(qkv, rel_k, bias_u, bias_v, D, W,
                                                                          rows_blocks);
     hip_check(hipGetLastError(), "attention rows / vT kernel launch");
     const size_t lds = core_lds_bytes((int)t);
     attention_prime();
     AttnQOut Q{q, scales_t, gsum_t, (int)((nseg * t + 15) / 16 * 16)};
-    const dim3 grid((unsigned)(D.tp / 16), (unsigned)h, (unsigned)nseg);
-    if (qout)
-        attn_core_kernel<true><<<grid, 64 * kCoreWaves, lds, st>>>(D, W, scaling, ctx, Q);
-    else
-        attn_core_kernel<false><<<grid, 64 * kCoreWaves, lds, st>>>(D, W, scaling, ctx, Q);
+    const dim3 grid((unsigned)(D.tp / 16 * h), 1, (unsigned)nseg);
+    // blocks per wave and batch: the smallest depth whose one batch covers the keys (nkb blocks) and the widest band
+    // (at most (t + 29) / 16 + 1 position blocks), at most 4
+    const int nblk = std::max((int)(D.tp / 16), (int)((t + 29) / 16 + 1));
+    const int kpf = std::min(4, (nblk + kCoreWaves - 1) / kCoreWaves);
+    auto launch = [&](auto kernel) { kernel<<<grid, 64 * kCoreWaves, lds, st>>>(D, W, scaling, ctx, Q); };
+    switch (kpf + (qout ? 4 : 0)) {
+        case 1: launch(attn_core_kernel<false, 1>); break;
+        case 2: launch(attn_core_kernel<false, 2>); break;
+        case 3: launch(attn_core_kernel<false, 3>); break;
+        case 4: launch(attn_core_kernel<false, 4>); break;
+        case 5: launch(attn_core_kernel<true, 1>); break;
+        case 6: launch(attn_core_kernel<true, 2>); break;
+        case 7: launch(attn_core_kernel<true, 3>); break;
+        default: launch(attn_core_kernel<true, 4>); break;
+    }
     hip_check(hipGetLastError(), "attention core kernel launch");
 }
 
