@@ -248,6 +248,7 @@ __global__ __launch_bounds__(64 * kCoreWaves, 2) void attn_core_kernel(AttnDims 
     const v4i av0 = *(const v4i *)qv, av1 = *(const v4i *)(qv + 64);
     // D element e of lane l: row 4*(l/16) + e, column l%16
     const int drow = 4 * aq, dcol = arow;
+    const float vsv = W.vs[h * kDh + wave * 16 + dcol];  // the context block's vT scale, for the epilogue
     const float4 qu4 = *(const float4 *)&W.qus[h * D.tp + i0 + drow];
     const float4 qv4 = *(const float4 *)&W.qvs[h * D.tp + i0 + drow];
     const float qus[4] = {qu4.x, qu4.y, qu4.z, qu4.w}, qvs[4] = {qv4.x, qv4.y, qv4.z, qv4.w};
@@ -444,7 +445,6 @@ __global__ __launch_bounds__(64 * kCoreWaves, 2) void attn_core_kernel(AttnDims 
     }
     {
         const int c = wave * 16 + dcol;
-        const float vsv = W.vs[h * kDh + c];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int r = drow + e;
