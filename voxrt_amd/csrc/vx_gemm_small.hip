@@ -779,9 +779,11 @@ bool gemm_small(const GemmArgs &a, hipStream_t st) {
     if (a.t1 - a.m_base > 1024 && forced != kForceSmall) return false;
     // the producer/consumer kernel by default for 16 or more groups (K >= 2048: FFN-down), where the fold of many
     // chunks overlaps the next chunk's loads and MFMAs (T = 125 / 338 / 750: 11.1 / 11.5 / 18.6 -> 9.2 / 9.3 / 16.9
-    // us); with 8 groups the four-wavefront kernel is as fast or faster
+    // us), and for AddScaled with 8 groups (o-proj, pw2: T = 338 / 750 4.69 / 6.46 -> 4.44 / 5.85 us, where the
+    // four-wavefront kernel or, from 512 tokens, split-K over groups ran); other 8-group shapes keep those kernels
     const int ws = overrides().small_ws.load(std::memory_order_relaxed);
-    if (grouped && (ws == 1 || (ws == 0 && a.ng >= 16 && !(fm && fn))) && launch_ws(a, false, fm, fn, st)) {
+    const bool ws_default = a.ng >= 16 || a.ep == VX_EP_ADD_SCALED;
+    if (grouped && (ws == 1 || (ws == 0 && ws_default && !(fm && fn))) && launch_ws(a, false, fm, fn, st)) {
         hip_check(hipGetLastError(), "tgemm_small_ws launch");
         return true;
     }
