@@ -474,6 +474,42 @@ def test_stream_groups_kernel_every_output(dev, orc, m, k, n_out, grid, tile):
                                                          f"ep={ep_kind} bias={with_bias}")
 
 
+@pytest.mark.parametrize("path", ["stream4", "stream8", "small", "small_ws"])
+def test_grouped_fold_with_zero_and_negative_scales(dev, orc, path):
+    """128-column groups whose products xs * ws are exact zeros of either sign or negative: weight scales of -0.0,
+    +0.0 and negative values, all-zero token rows (scale 1, codes 0) and a zero group inside a row, with old outputs
+    of -0.0 and +0.0 under AddScaled (whose result shows the sign of a zero fold). The kernels that form xs * ws on
+    the fp32 matrix cores (+0 for an exact zero product where the multiply gives -0) equal the oracle bit for bit."""
+    import voxrt_amd as vx
+
+    m, k, n_out, group = 300, 1024, 1024, 128
+    ng = k // group
+    trits, s16, x = _workload(orc, m, k, n_out, group, seed_cfg=11)
+    ws = orc.f16_to_f32(s16).reshape(n_out, ng).copy()
+    ws[0:16, 3] = -0.0
+    ws[16:32, 5] = 0.0
+    ws[32:48, :] = -ws[32:48, :]
+    ws[48, :] = -0.0
+    ws[49, :] = 0.0
+    x = x.copy()
+    x[[5, 77, 200, 299], :] = 0.0
+    x[10, 2 * group:3 * group] = 0.0
+    w = vx.TernaryMatrix.from_packed_f32(synth.pack_rows(trits), ws, n_out, k, group)
+    q, xs, _ = orc.quantize(x, group)
+    xa = vx.QuantAct.quantize(_t(x, dev), group)
+    base = np.zeros((m, n_out), np.float32)
+    base[::2, ::3] = -0.0
+    base[1::2, 1::5] = np.float32(0.25)
+    ov = {"stream4": dict(gemm="stream", stream_tile="4"), "stream8": dict(gemm="stream", stream_tile="8"),
+          "small": dict(gemm="small", small_ws="off"), "small_ws": dict(gemm="small", small_ws="on")}[path]
+    with vx.kernels.kernel_override(**ov):
+        for ep_kind, alpha in [(0, 0.0), (2, 0.5)]:
+            want = orc.gemm(trits, ws, q, xs, group, y=base.copy(), ep=ep_kind, alpha=alpha)
+            y = _t(base, dev)
+            vx.gemm_ep(w, xa, y, None, _ep_of(vx, ep_kind, alpha))
+            _assert_bits_equal(y.cpu().numpy(), want, f"signed-zero scales {path} ep={ep_kind}")
+
+
 @pytest.mark.parametrize("tile,group,m,k", [
     ("1x8", 0, 100, 1024), ("2x4", 0, 100, 256), ("2x8", 0, 53, 4096), ("3x2", 0, 100, 4096),
     ("3x4", 0, 338, 512), ("3x8", 0, 100, 1024), ("1x8", 0, 70, 2048), ("2x8", 0, 100, 2048),

@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256) void linear_f32_mfma_kernel(const float *__res
     const int l16 = lane & 15, lc = lane >> 4;                           // row in a block, running sum
     const int wt0 = (wv & 1) * 16 * WT, wo0 = (wv >> 1) * 16 * WO;       // the wavefront's blocks in the tile
     const int c4 = in_f / 4 * 4, nsteps = c4 / 4, nslab = (c4 + KS - 1) / KS;
-    typedef float v16f __attribute__((ext_vector_type(16)));
+
     v16f acc[WT][WO];
 #pragma unroll
     for (int i = 0; i < WT; i++)

@@ -15,6 +15,7 @@
 namespace vx {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 // Device weight matrix. Ternary matrices hold 2-bit codes (trit + 1) in the MFMA operand order; int8 matrices
 // hold the bytes themselves in the same block order. Rows are padded with zero weights and zero scales to a
