@@ -346,18 +346,18 @@ def test_encoder_batch_of_32_equals_single_segments(dev):
     enc.free()
 
 
-@pytest.mark.parametrize("t", [1, 29, 338, 750])
-def test_glu_dwconv_silu_quantize_equals_oracle(dev, orc, t):
+@pytest.mark.parametrize("t,k", [(1, 9), (29, 9), (338, 9), (750, 9), (29, 7), (338, 5)])
+def test_glu_dwconv_silu_quantize_equals_oracle(dev, orc, t, k):
     """The conv rows quantized for pointwise_conv2 in the same kernel (encoder.rs:605-625) equal the oracle's
     dwconv_bn_silu(glu(g)) quantized in 128-channel groups: codes, scales and code sums bit for bit, pad tokens
-    zero."""
+    zero. Kernel size 9 (the model's) runs the 8-row tiled kernel, other sizes the per-row kernel."""
     import torch
 
     from voxrt_amd import encoder as E
 
     d = 1024
     g = _x(t + 7, t, 2 * d, scale=2.0)
-    dw = _x(20, d, 9, scale=0.3)
+    dw = _x(20, d, k, scale=0.3)
     gamma, beta, mean = _x(21, d) * 0.1 + 1, _x(22, d) * 0.1, _x(23, d) * 0.1
     var = np.random.default_rng(24).uniform(0.5, 1.5, d).astype(np.float32)
     w_t, bias = orc.fold_bn(dw, gamma, beta, mean, var)
