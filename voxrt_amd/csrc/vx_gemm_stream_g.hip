@@ -329,7 +329,10 @@ bool gemm_stream_groups(const GemmArgs &a, int tokens_full, hipStream_t st) {
     g.nk = (int)nk;
     g.ng = (int)a.ng;
     const int cus = cu_count(), wpc = tb == 4 ? 2 : 1;  // workgroups per CU
-    if ((tokens_full / kBM) * g.n_nt < cus / 2 && forced == kForceNone) return false;  // too few tiles
+    // too few tiles of this kernel's height. Above 1024 tokens (no small-token kernel) a quarter of the CUs is
+    // enough: at 1500 / 4000 tokens and 1024 outputs its 88 / 248 tiles beat the LDS-staged kernel (o-proj 19.7 /
+    // 22.5 -> 17.3 / 19.0 us, FFN-down 49.9 / 54.3 -> 44.1 / 47.6 us)
+    if (g.ntiles < (a.t1 > 1024 ? cus / 4 : cus / 2) && forced == kForceNone) return false;
     int per_x = std::min(wpc * cus / 8, g.per_xcd);
     const int fg = overrides().stream_grid.load(std::memory_order_relaxed);  // workgroups: tests and tuning
     if (fg >= 8) per_x = std::min(fg / 8, g.per_xcd);
