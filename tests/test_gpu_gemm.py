@@ -546,11 +546,13 @@ def test_small_kernel_every_output(dev, orc, tile, group, m, k):
                                                          f"bias={with_bias}")
 
 
+@pytest.mark.parametrize("tile", ["2x4", "1x4"])
 @pytest.mark.parametrize("m,k", [(100, 1024), (338, 4096), (70, 2048), (338, 1024), (17, 4096)])
-def test_small_ws_kernel_every_output(dev, orc, m, k):
+def test_small_ws_kernel_every_output(dev, orc, m, k, tile):
     """The grouped small-token kernel with producer and consumer wavefronts (chains seeded with -gsum, int32 sums
     through two LDS planes, the fold one chunk behind), forced on ragged token counts with 8, 16 and 32 groups
-    (rings of 4 and 8 steps): each epilogue with and without bias, every output bit-exact."""
+    (rings of 4 and 8 steps) and with 32- and 16-token tiles: each epilogue with and without bias, every output
+    bit-exact."""
     import voxrt_amd as vx
 
     n_out, g = 256, 128
@@ -562,15 +564,15 @@ def test_small_ws_kernel_every_output(dev, orc, m, k):
     rng = synth.Lcg(61)
     base = ((rng.take(m * n_out) % 200).astype(np.float32) * np.float32(0.01) - np.float32(1.0)).reshape(m, n_out)
     bias = (rng.take(n_out) % 100).astype(np.float32) / np.float32(10.0)
-    with vx.kernels.kernel_override(gemm="small", small_ws="on"):
+    with vx.kernels.kernel_override(gemm="small", small_ws="on", small_tile=tile):
         for ep_kind, alpha in [(0, 0.0), (1, 0.0), (2, 0.5)]:
             want = orc.gemm(trits, ws, q, xs, g, y=base.copy(), ep=ep_kind, alpha=alpha)
             for with_bias in (False, True):
                 y = _t(base, dev)
                 vx.gemm_ep(w, xa, y, _t(bias, dev) if with_bias else None, _ep_of(vx, ep_kind, alpha))
                 exp = (want + bias[None, :]).astype(np.float32) if with_bias else want
-                _assert_bits_equal(y.cpu().numpy(), exp, f"small_ws G=128 {m}x{k}x{n_out} ep={ep_kind} "
-                                                         f"bias={with_bias}")
+                _assert_bits_equal(y.cpu().numpy(), exp, f"small_ws G=128 {m}x{k}x{n_out} tile={tile} "
+                                                         f"ep={ep_kind} bias={with_bias}")
 
 
 @pytest.mark.parametrize("tile", ["1x8", "2x8"])

@@ -712,12 +712,15 @@ bool launch_ws(const GemmArgs &a, bool qout, int fm, int fn, hipStream_t st) {
     if (a.ng != 8 && a.ng != 16 && a.ng != 32) return false;
     int mt = qout ? 1 : 2, nt = qout ? 8 : 4;
     if (fm) {
-        if (qout ? !((fm == 1 || fm == 2) && fn == 8) : !(fm == 2 && fn == 4)) return false;
+        if (qout ? !((fm == 1 || fm == 2) && fn == 8) : !((fm == 1 || fm == 2) && fn == 4)) return false;
         mt = fm;
         nt = fn;
     }
     if (a.out % (16 * nt) != 0 || (qout && a.ng != 8)) return false;
     const int64_t ntok = a.t1 - a.m_base;
+    // 16 x 64 tiles where 32 x 64 would leave more than half the CUs idle (T = 125: FFN-down 9.13 -> 8.45 us, o-proj
+    // 4.24 -> 3.89 us; at T = 338 the 32-token tile is faster, 9.4 against 11.0 us)
+    if (!qout && !fm && ((ntok + 31) / 32) * (a.out / (16 * nt)) < cu_count() / 2) mt = 1;
     const int n_mt = (int)((ntok + 16 * mt - 1) / (16 * mt)), tiles = n_mt * (int)(a.out / (16 * nt));
     const int per_xcd = (tiles + 7) / 8, grid = 8 * per_xcd;
     if (qout) {
@@ -726,9 +729,15 @@ bool launch_ws(const GemmArgs &a, bool qout, int fm, int fn, hipStream_t st) {
         else
             launch_ws_g<2, 8, 1, 4, 8>(a, grid, n_mt, per_xcd, tiles, st);
     } else if (a.ng == 8) {
-        launch_ws_g<2, 4, 2, 4, 8>(a, grid, n_mt, per_xcd, tiles, st);
+        if (mt == 1)
+            launch_ws_g<1, 4, 2, 4, 8>(a, grid, n_mt, per_xcd, tiles, st);
+        else
+            launch_ws_g<2, 4, 2, 4, 8>(a, grid, n_mt, per_xcd, tiles, st);
     } else {
-        launch_ws_g<2, 4, 2, 8, kMaxG>(a, grid, n_mt, per_xcd, tiles, st);
+        if (mt == 1)
+            launch_ws_g<1, 4, 2, 8, kMaxG>(a, grid, n_mt, per_xcd, tiles, st);
+        else
+            launch_ws_g<2, 4, 2, 8, kMaxG>(a, grid, n_mt, per_xcd, tiles, st);
     }
     return true;
 }
