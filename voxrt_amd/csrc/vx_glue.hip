@@ -582,6 +582,54 @@ __global__ __launch_bounds__(256) void dwconv2d_kernel(const float *__restrict__
     }
 }
 
+// dwconv2d_kernel for the model's 3x3 stride-2 stages: a block is one output time row of one segment, a thread one
+// channel; its nine weights stay in registers and it walks the output frequencies, each reading the two new input
+// columns of the three rows (the first column is the previous output's last), so an output costs 6 loads instead
+// of 18. Taps in the same order (kt outer, kf inner, out-of-range ones skipped), each o = o + w * x unfused.
+__global__ __launch_bounds__(256) void dwconv2d_k3s2_kernel(const float *__restrict__ x, int tc, int fc,
+                                                           const float *__restrict__ w, const float *__restrict__ b,
+                                                           int c, int t2, int f2, float *__restrict__ y) {
+    const int seg = blockIdx.x / t2, ot = blockIdx.x % t2;
+    x += (int64_t)seg * tc * fc * c;
+    y += ((int64_t)seg * t2 + ot) * f2 * c;
+    for (int ch = threadIdx.x; ch < c; ch += blockDim.x) {
+        float wk[9];
+#pragma unroll
+        for (int e = 0; e < 9; e++) wk[e] = w[e * c + ch];
+        const float bias = b[ch];
+        bool rv[3];
+        const float *xr[3];
+#pragma unroll
+        for (int kt = 0; kt < 3; kt++) {
+            const int it = 2 * ot + kt - 1;
+            rv[kt] = it >= 0 && it < tc;
+            xr[kt] = x + (int64_t)(rv[kt] ? it : 0) * fc * c + ch;
+        }
+        float prev[3] = {0.0f, 0.0f, 0.0f};  // column 2 of - 1 (of = 0: column -1, out of range)
+        for (int of = 0; of < f2; of++) {
+            const int f1 = 2 * of, f2c = 2 * of + 1;
+            const bool v0 = of > 0, v2 = f2c < fc;  // column 2 of - 1 and 2 of + 1 in range (2 of < fc always)
+            float cur1[3], cur2[3];
+#pragma unroll
+            for (int kt = 0; kt < 3; kt++) {
+                cur1[kt] = rv[kt] ? xr[kt][(int64_t)f1 * c] : 0.0f;
+                cur2[kt] = rv[kt] && v2 ? xr[kt][(int64_t)f2c * c] : 0.0f;
+            }
+            float o = bias;
+#pragma unroll
+            for (int kt = 0; kt < 3; kt++) {
+                if (!rv[kt]) continue;
+                if (v0) o = o + wk[kt * 3] * prev[kt];
+                o = o + wk[kt * 3 + 1] * cur1[kt];
+                if (v2) o = o + wk[kt * 3 + 2] * cur2[kt];
+            }
+#pragma unroll
+            for (int kt = 0; kt < 3; kt++) prev[kt] = cur2[kt];
+            y[(int64_t)of * c + ch] = o;
+        }
+    }
+}
+
 // Stage 0 and the first depthwise stage in one pass, without the stage-0 tensor in memory, for the model's shape (3x3
 // kernels, stride 2, NM mel bins: F1 = NM / 2 stage-0 frequencies, F2 = F1 / 2 depthwise outputs). A block is one
 // output time row ot2 of the depthwise stage, a thread one channel: it streams the stage-0 values of its channel
@@ -684,10 +732,15 @@ int64_t subsampling_seg(const float *feats, int64_t nseg, int64_t t, int64_t nm,
                                                                          (int)c, t1, t2, bbuf);
             hip_check(hipGetLastError(), "conv0 + dwconv2d kernel launch");
         } else {
-            dwconv2d_kernel<<<(unsigned)(nseg * t2 * f2), 256, 0, st>>>(a, tc, fc, (int)k, (int)s,
-                                                                          dw_w + (int64_t)stage * k * k * c,
-                                                                          dw_b + (int64_t)stage * c, (int)c, t2, f2,
-                                                                          bbuf);
+            if (k == 3 && s == 2)
+                dwconv2d_k3s2_kernel<<<(unsigned)(nseg * t2), 256, 0, st>>>(a, tc, fc, dw_w + (int64_t)stage * 9 * c,
+                                                                             dw_b + (int64_t)stage * c, (int)c, t2,
+                                                                             f2, bbuf);
+            else
+                dwconv2d_kernel<<<(unsigned)(nseg * t2 * f2), 256, 0, st>>>(a, tc, fc, (int)k, (int)s,
+                                                                              dw_w + (int64_t)stage * k * k * c,
+                                                                              dw_b + (int64_t)stage * c, (int)c, t2,
+                                                                              f2, bbuf);
             hip_check(hipGetLastError(), "dwconv2d kernel launch");
         }
         linear_f32(bbuf, nseg * t2 * f2, c, pw_w + (int64_t)stage * c * c, pw_b + (int64_t)stage * c, c, a, true,
