@@ -155,7 +155,10 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
                                                         const float *__restrict__ lb2) {
     static_assert(MODE != 2 || LN, "MODE 2 is two LayerNorms");
     constexpr int inp = NC * 1024;
-    __shared__ __attribute__((aligned(16))) float srow[LN ? 4 : 1][LN ? inp : 4];
+    // the transposed row of each wavefront: 8 residue rows of inp / 8 values, each padded by 4 floats so that the
+    // 16-byte reads of lanes 0-7 fall on distinct LDS banks
+    constexpr int KLP = inp / 8 + 4;
+    __shared__ __attribute__((aligned(16))) float srow[LN ? 4 : 1][LN ? 8 * KLP : 4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + w;
     if (t >= np) return;
@@ -199,28 +202,30 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
     }
     // LayerNorm of the row in v, in place: statistics in the reference's order over the row staged in LDS
     auto ln_pass = [&](const float4 (&G)[LN ? NC : 1][4], const float4 (&B)[LN ? NC : 1][4]) __attribute__((always_inline)) {
-        // the row transposed by column residue: T[j][k] = x[8k + j], so that the running sum of residue j (the
-        // reference's lane j of row_mean_var_portable) walks contiguous memory
+        // the row transposed by column residue: T[j * KLP + k] = x[8k + j], so that the running sum of residue j
+        // (the reference's lane j of row_mean_var_portable) walks contiguous memory
         constexpr int KL = inp / 8;
         float *T = srow[w];
 #pragma unroll
         for (int c = 0; c < NC; c++)
 #pragma unroll
             for (int j = 0; j < 8; j++)
-                *(float2 *)(T + j * KL + c * 128 + 2 * lane) = make_float2(v[c][j], v[c][8 + j]);
+                *(float2 *)(T + j * KLP + c * 128 + 2 * lane) = make_float2(v[c][j], v[c][8 + j]);
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's row is in LDS
         __builtin_amdgcn_wave_barrier();
         float mean, linv;
         // lane j < 8 keeps the running sum of columns j, j+8, j+16, ... in that order. Each 128-value stretch of
         // its column is read from LDS in one batch before the dependent additions start.
         float s = 0.0f;
-        if (lane < 8) {
-            const float *r = T + lane * KL;
+        if constexpr (KL == 128) {
+            // one stretch (1024 columns): all 32 reads issue before the first addition, and the stretch stays in
+            // registers for the variance chain
+            float4 f[32];
+            if (lane < 8) {
+                const float *r = T + lane * KLP;
 #pragma unroll
-            for (int k0 = 0; k0 < KL; k0 += 128) {
-                float4 f[32];
-#pragma unroll
-                for (int k = 0; k < 32; k++) f[k] = *(const float4 *)(r + k0 + 4 * k);
+                for (int k = 0; k < 32; k++) f[k] = *(const float4 *)(r + 4 * k);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int k = 0; k < 32; k++) {
                     s += f[k].x;
@@ -229,16 +234,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
                     s += f[k].w;
                 }
             }
-        }
-        mean = hsum8_lanes(s) / (float)inp;
-        float qs = 0.0f;
-        if (lane < 8) {
-            const float *r = T + lane * KL;
-#pragma unroll
-            for (int k0 = 0; k0 < KL; k0 += 128) {
-                float4 f[32];
-#pragma unroll
-                for (int k = 0; k < 32; k++) f[k] = *(const float4 *)(r + k0 + 4 * k);
+            mean = hsum8_lanes(s) / (float)inp;
+            float qs = 0.0f;
+            if (lane < 8) {
 #pragma unroll
                 for (int k = 0; k < 32; k++) {
                     float a = f[k].x - mean;
@@ -251,9 +249,50 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
                     qs = __builtin_fmaf(a, a, qs);
                 }
             }
+            const float var = hsum8_lanes(qs) / (float)inp;
+            linv = 1.0f / __builtin_sqrtf(var + 1e-5f);
+        } else {
+            if (lane < 8) {
+                const float *r = T + lane * KLP;
+#pragma unroll
+                for (int k0 = 0; k0 < KL; k0 += 128) {
+                    float4 f[32];
+#pragma unroll
+                    for (int k = 0; k < 32; k++) f[k] = *(const float4 *)(r + k0 + 4 * k);
+#pragma unroll
+                    for (int k = 0; k < 32; k++) {
+                        s += f[k].x;
+                        s += f[k].y;
+                        s += f[k].z;
+                        s += f[k].w;
+                    }
+                }
+            }
+            mean = hsum8_lanes(s) / (float)inp;
+            float qs = 0.0f;
+            if (lane < 8) {
+                const float *r = T + lane * KLP;
+#pragma unroll
+                for (int k0 = 0; k0 < KL; k0 += 128) {
+                    float4 f[32];
+#pragma unroll
+                    for (int k = 0; k < 32; k++) f[k] = *(const float4 *)(r + k0 + 4 * k);
+#pragma unroll
+                    for (int k = 0; k < 32; k++) {
+                        float a = f[k].x - mean;
+                        qs = __builtin_fmaf(a, a, qs);
+                        a = f[k].y - mean;
+                        qs = __builtin_fmaf(a, a, qs);
+                        a = f[k].z - mean;
+                        qs = __builtin_fmaf(a, a, qs);
+                        a = f[k].w - mean;
+                        qs = __builtin_fmaf(a, a, qs);
+                    }
+                }
+            }
+            const float var = hsum8_lanes(qs) / (float)inp;
+            linv = 1.0f / __builtin_sqrtf(var + 1e-5f);
         }
-        const float var = hsum8_lanes(qs) / (float)inp;
-        linv = 1.0f / __builtin_sqrtf(var + 1e-5f);
 #pragma unroll
         for (int c = 0; c < NC; c++) {
 #pragma unroll
