@@ -309,22 +309,22 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict
 // instruction is one 4-column step for 16 tokens x 16 outputs:
 //   lane l supplies A = x[token l % 16][4s + l / 16] and B = w[output l % 16][4s + l / 16];
 //   D register r of lane l is running sum r / 4 of token 4 * (l / 16) + r % 4 and output l % 16.
-// The slabs of x and w are staged in LDS de-interleaved by running sum, [c][row][step] with a row pitch of 36
+// The slabs of x and w are staged in LDS de-interleaved by running sum, [c][row][step] with a row pitch of KS/4 + 4
 // floats (16 consecutive rows of one c start in distinct bank quads), so one 16-byte read gives a lane four steps.
+// Two LDS buffers and two register sets: slab s + 2 is fetched into registers while slab s is multiplied, slab s + 1
+// is written to the other buffer after it, one barrier per slab, so a fetch has two slabs of MFMAs to arrive.
 // Only the steps below in_f / 4 are issued (padding is never accumulated: fma(0, 0, -0) would be +0); the
 // unfused tail and (hsum4 + tail) + bias follow in the epilogue. A workgroup of four wavefronts (2 x 2) owns
 // (32 WT) tokens x (32 WO) outputs, a wavefront WT x WO blocks of 16 x 16.
-constexpr int kLinMK = 128;  // slab columns (32 steps)
-
-template <bool RELU, int WT, int WO>
+template <bool RELU, int WT, int WO, int KS>
 __global__ __launch_bounds__(256) void linear_f32_mfma_kernel(const float *__restrict__ x, int n, int in_f,
                                                              const float *__restrict__ w,
                                                              const float *__restrict__ b, int out_f,
                                                              float *__restrict__ y) {
-    constexpr int BM = 32 * WT, BN = 32 * WO, KS = kLinMK, SP = KS / 4 + 4;  // SP: row pitch (floats)
-    constexpr int QX = BM * KS / 16 / 256, QW = BN * KS / 16 / 256;           // 16-column pieces per thread
+    constexpr int BM = 32 * WT, BN = 32 * WO, SP = KS / 4 + 4;      // SP: row pitch (floats)
+    constexpr int QX = BM * KS / 16 / 256, QW = BN * KS / 16 / 256;  // 16-column pieces per thread
     static_assert(QX >= 1 && QW >= 1, "a thread stages at least one piece of each operand");
-    __shared__ __attribute__((aligned(16))) float sx[4][BM][SP], sw[4][BN][SP];
+    __shared__ __attribute__((aligned(16))) float sx[2][4][BM][SP], sw[2][4][BN][SP];
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t0 = blockIdx.y * BM, o0 = blockIdx.x * BN;
     const int l16 = lane & 15, lc = lane >> 4;                           // row in a block, running sum
@@ -339,57 +339,56 @@ __global__ __launch_bounds__(256) void linear_f32_mfma_kernel(const float *__res
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
     // staging: piece p of an operand is row p / (KS / 16), columns 16 (p % (KS / 16)) .. + 15 of the slab, loaded as
-    // four quads and written as four quads of consecutive steps, one per running sum
-    float4 px[QX][4], pq[QW][4];
-    auto fetch = [&](int k0) __attribute__((always_inline)) {
+    // four quads and written as four quads of consecutive steps, one per running sum. Quads at or past c4 are
+    // loaded from column c4 - 4 (in bounds, no branch around the load, so the loads of a fetch stay in flight
+    // together) and written as zeros.
+    float4 px[2][QX][4], pq[2][QW][4];
+    auto fetch = [&](int set, int k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < QX; q++) {
             const int p = tid + 256 * q, r = p / (KS / 16), c = k0 + 16 * (p % (KS / 16));
-            const float *src = x + (int64_t)min(t0 + r, n - 1) * in_f + c;
+            const float *src = x + (int64_t)min(t0 + r, n - 1) * in_f;
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                px[q][j] = c + 4 * j < c4 ? *(const float4 *)(src + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int j = 0; j < 4; j++) px[set][q][j] = *(const float4 *)(src + min(c + 4 * j, c4 - 4));
         }
 #pragma unroll
         for (int q = 0; q < QW; q++) {
             const int p = tid + 256 * q, r = p / (KS / 16), c = k0 + 16 * (p % (KS / 16));
-            const float *src = w + (int64_t)min(o0 + r, out_f - 1) * in_f + c;
+            const float *src = w + (int64_t)min(o0 + r, out_f - 1) * in_f;
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                pq[q][j] = c + 4 * j < c4 ? *(const float4 *)(src + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int j = 0; j < 4; j++) pq[set][q][j] = *(const float4 *)(src + min(c + 4 * j, c4 - 4));
         }
     };
-    auto stash = [&]() __attribute__((always_inline)) {
+    // stash unit u < 4 (QX + QW): running-sum plane u % 4 of piece (u / 4) of x, then of w; register set `set` ->
+    // LDS buffer `set`
+    constexpr int NU = 4 * (QX + QW);
+    auto stash_unit = [&](int set, int k0, int u) __attribute__((always_inline)) {
+        const bool isx = u < 4 * QX;
+        const int q = (isx ? u : u - 4 * QX) / 4, c = u % 4;
+        const int p = tid + 256 * q, r = p / (KS / 16), s = 4 * (p % (KS / 16)), col = k0 + 4 * s;
+        float e[4];
 #pragma unroll
-        for (int q = 0; q < QX; q++) {
-            const int p = tid + 256 * q, r = p / (KS / 16), s = 4 * (p % (KS / 16));
-            *(float4 *)&sx[0][r][s] = make_float4(px[q][0].x, px[q][1].x, px[q][2].x, px[q][3].x);
-            *(float4 *)&sx[1][r][s] = make_float4(px[q][0].y, px[q][1].y, px[q][2].y, px[q][3].y);
-            *(float4 *)&sx[2][r][s] = make_float4(px[q][0].z, px[q][1].z, px[q][2].z, px[q][3].z);
-            *(float4 *)&sx[3][r][s] = make_float4(px[q][0].w, px[q][1].w, px[q][2].w, px[q][3].w);
+        for (int j = 0; j < 4; j++) {
+            const float4 v = isx ? px[set][q][j] : pq[set][q][j];
+            const float comp = c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
+            e[j] = col + 4 * j < c4 ? comp : 0.0f;
         }
-#pragma unroll
-        for (int q = 0; q < QW; q++) {
-            const int p = tid + 256 * q, r = p / (KS / 16), s = 4 * (p % (KS / 16));
-            *(float4 *)&sw[0][r][s] = make_float4(pq[q][0].x, pq[q][1].x, pq[q][2].x, pq[q][3].x);
-            *(float4 *)&sw[1][r][s] = make_float4(pq[q][0].y, pq[q][1].y, pq[q][2].y, pq[q][3].y);
-            *(float4 *)&sw[2][r][s] = make_float4(pq[q][0].z, pq[q][1].z, pq[q][2].z, pq[q][3].z);
-            *(float4 *)&sw[3][r][s] = make_float4(pq[q][0].w, pq[q][1].w, pq[q][2].w, pq[q][3].w);
-        }
+        *(float4 *)(isx ? &sx[set][c][r][s] : &sw[set][c][r][s]) = make_float4(e[0], e[1], e[2], e[3]);
     };
-    fetch(0);
-    for (int sl = 0; sl < nslab; sl++) {
-        if (sl > 0) __syncthreads();  // every wavefront is done with the previous slab
-        stash();
-        __syncthreads();
-        if (sl + 1 < nslab) fetch((sl + 1) * KS);
+    auto stash = [&](int set, int k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NU; u++) stash_unit(set, k0, u);
+    };
+    // the steps of slab sl from LDS buffer `buf`, and the stash of register set `sset` (slab at column sk0) into the
+    // other buffer: in a whole slab its units follow the MFMAs of each quad, so that they issue while those run
+    auto compute = [&](int buf, int sl, int sset, int sk0) __attribute__((always_inline)) {
         const int sn = min(KS / 4, nsteps - sl * (KS / 4));  // steps in this slab
         auto quad = [&](int s4) __attribute__((always_inline)) {  // steps s4 .. s4 + 3
             float4 xa[WT], wa[WO];
 #pragma unroll
-            for (int i = 0; i < WT; i++) xa[i] = *(const float4 *)&sx[lc][wt0 + 16 * i + l16][s4];
+            for (int i = 0; i < WT; i++) xa[i] = *(const float4 *)&sx[buf][lc][wt0 + 16 * i + l16][s4];
 #pragma unroll
-            for (int j = 0; j < WO; j++) wa[j] = *(const float4 *)&sw[lc][wo0 + 16 * j + l16][s4];
+            for (int j = 0; j < WO; j++) wa[j] = *(const float4 *)&sw[buf][lc][wo0 + 16 * j + l16][s4];
 #pragma unroll
             for (int e = 0; e < 4; e++)
 #pragma unroll
@@ -406,14 +405,71 @@ __global__ __launch_bounds__(256) void linear_f32_mfma_kernel(const float *__res
             for (int i = 0; i < WT; i++)
 #pragma unroll
                 for (int j = 0; j < WO; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x1f32(sx[lc][wt0 + 16 * i + l16][s],
-                                                                    sw[lc][wo0 + 16 * j + l16][s], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x1f32(sx[buf][lc][wt0 + 16 * i + l16][s],
+                                                                    sw[buf][lc][wo0 + 16 * j + l16][s], acc[i][j],
+                                                                    0, 0, 0);
         };
         int s = 0;
-#pragma unroll 2
-        for (; s + 4 <= sn; s += 4) quad(s);
-        for (; s < sn; s++) single(s);
+        if (sn == KS / 4) {
+            // a whole slab: unrolled, the LDS reads of quad q + RA issued before the MFMAs of quad q (two quads
+            // ahead for one block per wavefront, one for four blocks, whose quad has 16 MFMAs)
+            constexpr int NQ = KS / 16, RA = WT * WO >= 4 ? 1 : 2;
+            float4 xr[RA + 1][WT], wr[RA + 1][WO];
+            auto rd = [&](int slot, int s4) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < WT; i++) xr[slot][i] = *(const float4 *)&sx[buf][lc][wt0 + 16 * i + l16][s4];
+#pragma unroll
+                for (int j = 0; j < WO; j++) wr[slot][j] = *(const float4 *)&sw[buf][lc][wo0 + 16 * j + l16][s4];
+            };
+#pragma unroll
+            for (int q = 0; q < RA; q++) rd(q, 4 * q);
+#pragma unroll
+            for (int q = 0; q < NQ; q++) {
+                if (q + RA < NQ) rd((q + RA) % (RA + 1), 4 * (q + RA));
+                __builtin_amdgcn_sched_barrier(0);  // the scheduler would sink the reads to their MFMAs
+                const int sl3 = q % (RA + 1);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int i = 0; i < WT; i++)
+#pragma unroll
+                        for (int j = 0; j < WO; j++) {
+                            const float4 xa = xr[sl3][i], wa = wr[sl3][j];
+                            const float av = e == 0 ? xa.x : e == 1 ? xa.y : e == 2 ? xa.z : xa.w;
+                            const float bv = e == 0 ? wa.x : e == 1 ? wa.y : e == 2 ? wa.z : wa.w;
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x1f32(av, bv, acc[i][j], 0, 0, 0);
+                        }
+                constexpr int UPQ = (NU + NQ - 1) / NQ;
+#pragma unroll
+                for (int u = q * UPQ; u < (q + 1) * UPQ; u++)
+                    if (u < NU) stash_unit(sset, sk0, u);
+            }
+        } else {
+            for (; s + 4 <= sn; s += 4) quad(s);
+            for (; s < sn; s++) single(s);
+            stash(sset, sk0);
+        }
+    };
+    // slab k lives in register set k % 2 and LDS buffer k % 2. The fetches and stashes past the last slab repeat
+    // it (in bounds, never multiplied), so every slab issues the same loads and the counter waits stay exact.
+    fetch(0, 0);
+    fetch(1, min(1, nslab - 1) * KS);
+    __builtin_amdgcn_sched_barrier(0);
+    stash(0, 0);
+    __syncthreads();
+    auto slab = [&](auto Pc, int sl) __attribute__((always_inline)) {
+        constexpr int P = decltype(Pc)::value;            // sl % 2
+        fetch(P, min(sl + 2, nslab - 1) * KS);            // set P held slab sl, in LDS since the last barrier
+        __builtin_amdgcn_sched_barrier(0);
+        compute(P, sl, P ^ 1, min(sl + 1, nslab - 1) * KS);  // buffer P ^ 1 was last read before the last barrier
+        __syncthreads();
+    };
+    int sl = 0;
+    for (; sl + 1 < nslab; sl += 2) {
+        slab(IC<0>{}, sl);
+        slab(IC<1>{}, sl + 1);
     }
+    if (sl < nslab) slab(IC<0>{}, sl);
     // epilogue: lane l holds, for output o0 + wo0 + 16 j + l % 16, tokens t0 + wt0 + 16 i + 4 (l / 16) + e
 #pragma unroll
     for (int j = 0; j < WO; j++) {
@@ -491,15 +547,17 @@ void linear_f32(const float *x, int64_t n, int64_t in_f, const float *w, const f
         if (aligned && kind > 0) {
             const int wt = kind / 10 % 10, wo = kind % 10;
             const dim3 grid((unsigned)((out_f + 32 * wo - 1) / (32 * wo)), (unsigned)((n + 32 * wt - 1) / (32 * wt)));
-#define VX_LINM(WT, WO)                                                                                           \
-    (relu ? linear_f32_mfma_kernel<true, WT, WO> : linear_f32_mfma_kernel<false, WT, WO>)<<<grid, 256, 0, st>>>(   \
+#define VX_LINM(WT, WO, KS)                                                                                       \
+    (relu ? linear_f32_mfma_kernel<true, WT, WO, KS> : linear_f32_mfma_kernel<false, WT, WO, KS>)<<<grid, 256, 0, \
+                                                                                                   st>>>(         \
         x, (int)n, (int)in_f, w, b, (int)out_f, y)
+            // slabs of 64 columns for 64 x 64 tiles (two workgroups of 80 KB LDS per CU), else 128
             if (wt == 2 && wo == 2)
-                VX_LINM(2, 2);
+                VX_LINM(2, 2, 64);
             else if (wt == 2)
-                VX_LINM(2, 1);
+                VX_LINM(2, 1, 128);
             else
-                VX_LINM(1, 1);
+                VX_LINM(1, 1, 128);
 #undef VX_LINM
         } else {
             auto k = relu ? linear_f32_kernel<true> : linear_f32_kernel<false>;
