@@ -58,11 +58,8 @@ __device__ inline int8_t q_code(float x, float inv) {
     return (int8_t)(int)v;
 }
 
-__device__ inline float wave_max(float m) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    return m;
-}
+// max over the wavefront of non-negative values (every lane active)
+__device__ inline float wave_max(float m) { return lane_group_max<64>(m); }
 
 // Quantize the 128 values a (two per lane: columns 2*lane, 2*lane+1) into dst[128]; returns the scale.
 __device__ inline float quant128(float a0, float a1, int lane, int8_t *dst) {

@@ -300,8 +300,7 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
             float m = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(__int_as_float(lo[j])), fabsf(__int_as_float(hi[j]))));
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            m = lane_group_max<16>(m);
             const float s = m == 0.0f ? 1.0f : m / 127.0f;
             const float inv = 1.0f / s;
             uint32_t w0 = 0, w1 = 0;
@@ -313,8 +312,7 @@ __global__ __launch_bounds__(256, (MT == 1 && NT == 8 && D <= 4 && (!GROUPED || 
                 w0 |= (uint32_t)(uint8_t)c0 << (8 * j);
                 w1 |= (uint32_t)(uint8_t)c1 << (8 * j);
             }
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            sum = lane_group_sum<16>(sum);
             const int64_t gi = (int64_t)(o0 / 128) * a.np + t;
             if (t < a.n) {
                 *(uint2 *)(a.qo + (int64_t)t * a.out + o0) = make_uint2(w0, w1);
@@ -543,8 +541,7 @@ __global__ __launch_bounds__(512, NPL == 1 ? 2 : 1) void tgemm_small_ws_kernel(c
             float m = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(__int_as_float(lo[j])), fabsf(__int_as_float(hi[j]))));
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            m = lane_group_max<16>(m);
             const float s = m == 0.0f ? 1.0f : m / 127.0f;
             const float inv = 1.0f / s;
             uint32_t w0 = 0, w1 = 0;
@@ -556,8 +553,7 @@ __global__ __launch_bounds__(512, NPL == 1 ? 2 : 1) void tgemm_small_ws_kernel(c
                 w0 |= (uint32_t)(uint8_t)q0 << (8 * j);
                 w1 |= (uint32_t)(uint8_t)q1 << (8 * j);
             }
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            sum = lane_group_sum<16>(sum);
             const int64_t gi = (int64_t)(o0 / 128) * a.np + t;
             if (t < a.n) {
                 *(uint2 *)(a.qo + (int64_t)t * a.out + o0) = make_uint2(w0, w1);

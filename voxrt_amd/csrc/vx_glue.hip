@@ -86,8 +86,7 @@ __global__ __launch_bounds__(256) void glu_dwconv_silu_quant_kernel(const float 
     }
     const float v = silu_fast(acc);
     float m = fabsf(v);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    m = lane_group_max<64>(m);
     if (lane == 0) smax[wv] = m;
     __syncthreads();
     m = fmaxf(smax[wv & ~1], smax[wv | 1]);
@@ -96,8 +95,7 @@ __global__ __launch_bounds__(256) void glu_dwconv_silu_quant_kernel(const float 
     const int8_t code = code_of(v, inv);
     q[(int64_t)row * d + c] = code;
     int sum = code;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    sum = lane_group_sum<64>(sum);
     if (lane == 0) ssum[wv] = sum;
     __syncthreads();
     if ((threadIdx.x & 127) == 0) {
