@@ -700,9 +700,9 @@ void launch_ws_g(const GemmArgs &a, int grid, int n_mt, int per_xcd, int ntiles,
     }
 }
 
-// The producer/consumer kernel for 8 groups (K = 1024, a ring of 4 steps per producer) or 16 / 32 groups (a ring
-// of 8): 32 x 64 tiles with two LDS planes for y, 16 x 128 or 32 x 128 tiles with one plane for the quantized
-// output (the next GEMM's activations, 8 groups only). Launches nothing and returns false for other shapes or a
+// The producer/consumer kernel for 8 groups (K = 1024, a ring of 2 steps per producer) or 16 / 32 groups (a ring
+// of 4): 32 x 64 tiles with two LDS planes for y, 16 x 128 or 32 x 128 tiles with one plane for the quantized output
+// (the next GEMM's activations, 8 groups only, a ring of 4). Launches nothing and returns false for other shapes or a
 // forced tile it is not built for.
 bool launch_ws(const GemmArgs &a, bool qout, int fm, int fn, hipStream_t st) {
     if (a.ng != 8 && a.ng != 16 && a.ng != 32) return false;
@@ -725,15 +725,19 @@ bool launch_ws(const GemmArgs &a, bool qout, int fm, int fn, hipStream_t st) {
         else
             launch_ws_g<2, 8, 1, 4, 8>(a, grid, n_mt, per_xcd, tiles, st);
     } else if (a.ng == 8) {
+        // shallow rings: the loads of the whole workgroup at its start queue behind each other, so a deep ring
+        // delays the first chunk; inside the encoder (operands not in L2) K = 4096 keeps two chunks in flight
+        // (encoder T = 338 / 750: rings 4 and 8 -> 2 and 4, 3.049 / 4.852 -> 3.024 / 4.663 ms; alone, o-proj at
+        // T = 338: 4.48 -> 4.24 us)
         if (mt == 1)
-            launch_ws_g<1, 4, 2, 4, 8>(a, grid, n_mt, per_xcd, tiles, st);
+            launch_ws_g<1, 4, 2, 2, 8>(a, grid, n_mt, per_xcd, tiles, st);
         else
-            launch_ws_g<2, 4, 2, 4, 8>(a, grid, n_mt, per_xcd, tiles, st);
+            launch_ws_g<2, 4, 2, 2, 8>(a, grid, n_mt, per_xcd, tiles, st);
     } else {
         if (mt == 1)
-            launch_ws_g<1, 4, 2, 8, kMaxG>(a, grid, n_mt, per_xcd, tiles, st);
+            launch_ws_g<1, 4, 2, 4, kMaxG>(a, grid, n_mt, per_xcd, tiles, st);
         else
-            launch_ws_g<2, 4, 2, 8, kMaxG>(a, grid, n_mt, per_xcd, tiles, st);
+            launch_ws_g<2, 4, 2, 4, kMaxG>(a, grid, n_mt, per_xcd, tiles, st);
     }
     return true;
 }
