@@ -163,8 +163,11 @@ def test_linear_f32_matrix_cores_on_special_operands(dev, orc, kernel):
     assert same.all(), f"{(~same).sum()} differ, first {np.argwhere(~same)[0]}"
 
 
-@pytest.mark.parametrize("t,n_mels,c,d", [(41, 40, 16, 96), (2704, 128, 256, 1024)])
+@pytest.mark.parametrize("t,n_mels,c,d", [(41, 40, 16, 96), (2704, 128, 256, 1024), (9, 128, 16, 32),
+                                          (130, 128, 40, 64), (137, 128, 300, 64), (141, 128, 24, 32)])
 def test_subsampling_equals_oracle(dev, orc, t, n_mels, c, d):
+    """128 mel bins run the first stage fused into the first depthwise stage: 3 to 676 output rows, even and odd
+    row counts, and more channels than threads (300)."""
     from voxrt_amd import encoder as E
 
     sp = synth.synth_subsampling(d=d, c=c, n_mels=n_mels)

@@ -551,7 +551,7 @@ def test_small_kernel_every_output(dev, orc, tile, group, m, k):
 def test_small_ws_kernel_every_output(dev, orc, m, k, tile):
     """The grouped small-token kernel with producer and consumer wavefronts (chains seeded with -gsum, int32 sums
     through two LDS planes, the fold one chunk behind), forced on ragged token counts with 8, 16 and 32 groups
-    (rings of 4 and 8 steps) and with 32- and 16-token tiles: each epilogue with and without bias, every output
+    (rings of 2 and 4 steps) and with 32- and 16-token tiles: each epilogue with and without bias, every output
     bit-exact."""
     import voxrt_amd as vx
 

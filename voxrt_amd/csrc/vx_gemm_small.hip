@@ -714,9 +714,14 @@ bool launch_ws(const GemmArgs &a, bool qout, int fm, int fn, hipStream_t st) {
     }
     if (a.out % (16 * nt) != 0 || (qout && a.ng != 8)) return false;
     const int64_t ntok = a.t1 - a.m_base;
-    // 16 x 64 tiles where 32 x 64 would leave more than half the CUs idle (T = 125: FFN-down 9.13 -> 8.45 us, o-proj
-    // 4.24 -> 3.89 us; at T = 338 the 32-token tile is faster, 9.4 against 11.0 us)
-    if (!qout && !fm && ((ntok + 31) / 32) * (a.out / (16 * nt)) < cu_count() / 2) mt = 1;
+    // 16 x 64 tiles for Store (q|k|v, pw1 at T = 338: 7.56 / 5.56 -> 7.06 / 5.22 us with 32 x 64 tiles), and for
+    // AddScaled where 32 x 64 tiles would leave more than half the CUs idle (T = 125: FFN-down 9.13 -> 8.45 us) or
+    // give every CU more than one and a half (T = 750: FFN-down, o-proj 13.38 / 5.71 -> 12.28 / 5.36 us); in
+    // between (T = 338) the 32-token tile is faster (FFN-down 8.63 against 9.86 us)
+    if (!qout && !fm) {
+        const int64_t t32 = ((ntok + 31) / 32) * (a.out / (16 * nt));
+        if (a.ep != VX_EP_ADD_SCALED || t32 < cu_count() / 2 || 2 * t32 >= 3 * (int64_t)cu_count()) mt = 1;
+    }
     const int n_mt = (int)((ntok + 16 * mt - 1) / (16 * mt)), tiles = n_mt * (int)(a.out / (16 * nt));
     const int per_xcd = (tiles + 7) / 8, grid = 8 * per_xcd;
     if (qout) {
@@ -786,13 +791,12 @@ bool gemm_small(const GemmArgs &a, hipStream_t st) {
     const int fm = ft >> 4, fn = ft & 15;
     // up to 1024 tokens; longer token ranges go to the kernels built for throughput
     if (a.t1 - a.m_base > 1024 && forced != kForceSmall) return false;
-    // the producer/consumer kernel by default for 16 or more groups (K >= 2048: FFN-down), where the fold of many
-    // chunks overlaps the next chunk's loads and MFMAs (T = 125 / 338 / 750: 11.1 / 11.5 / 18.6 -> 9.2 / 9.3 / 16.9
-    // us), and for AddScaled with 8 groups (o-proj, pw2: T = 338 / 750 4.69 / 6.46 -> 4.44 / 5.85 us, where the
-    // four-wavefront kernel or, from 512 tokens, split-K over groups ran); other 8-group shapes keep those kernels
+    // the producer/consumer kernel by default for 8, 16 or 32 groups: the fold of one chunk overlaps the next
+    // chunk's loads and MFMAs (FFN-down, T = 125 / 338 / 750: 11.1 / 11.5 / 18.6 -> 9.2 / 9.3 / 16.9 us; o-proj
+    // T = 338 / 750: 4.69 / 6.46 -> 4.44 / 5.85 us; q|k|v T = 338 / 750: 8.08 / 13.09 -> 7.06 / 10.83 us, where the
+    // four-wavefront kernel or split-K over groups ran); other group counts keep those kernels
     const int ws = overrides().small_ws.load(std::memory_order_relaxed);
-    const bool ws_default = a.ng >= 16 || a.ep == VX_EP_ADD_SCALED;
-    if (grouped && (ws == 1 || (ws == 0 && ws_default && !(fm && fn))) && launch_ws(a, false, fm, fn, st)) {
+    if (grouped && (ws == 1 || (ws == 0 && !(fm && fn))) && launch_ws(a, false, fm, fn, st)) {
         hip_check(hipGetLastError(), "tgemm_small_ws launch");
         return true;
     }
