@@ -177,12 +177,32 @@ __device__ inline void attn_vt16_block(int blk, const float *__restrict__ qkv, c
 }
 
 // The relative rows of nl layers in one launch (their projections depend on t and the weights only): layer blockIdx.y
-// reads columns [l*d, (l+1)*d) of rel_k (row pitch D.rel_ld) and writes rq + l * h*rp*dh, rs + l * h*rp.
+// reads columns [l*d, (l+1)*d) of rel_k (row pitch D.rel_ld) and writes rq + l * h*rp*dh, rs + l * h*rp. A wavefront
+// quantizes kRelPerWave consecutive rows r = h * rp + p, their loads issued together (one row per wavefront made
+// 135K wavefronts for 24 layers at T = 338, whose launch and single load each dominated).
+constexpr int kRelPerWave = 8;
 __global__ __launch_bounds__(256) void attn_rel_kernel(const float *__restrict__ rel_k, AttnDims D, int8_t *rq,
                                                       float *rs) {
-    const int l = blockIdx.y;
-    attn_rel_item((int)blockIdx.x * 4 + (threadIdx.x >> 6), rel_k + (int64_t)l * D.d, D,
-                  rq + (int64_t)l * D.h * D.rp * kDh, rs + (int64_t)l * D.h * D.rp);
+    const int l = blockIdx.y, lane = threadIdx.x & 63, nr = D.h * D.rp;
+    const int r0 = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * kRelPerWave;
+    if (r0 >= nr) return;  // uniform per wavefront
+    rel_k += (int64_t)l * D.d;
+    rq += (int64_t)l * nr * kDh;
+    rs += (int64_t)l * nr;
+    float2 v[kRelPerWave];
+#pragma unroll
+    for (int j = 0; j < kRelPerWave; j++) {
+        const int r = r0 + j, h = r / D.rp, p = r % D.rp;
+        v[j] = r < nr && p < D.np ? *(const float2 *)(rel_k + (int64_t)p * D.rel_ld + h * kDh + 2 * lane)
+                                  : make_float2(0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < kRelPerWave; j++) {
+        const int r = r0 + j;
+        if (r >= nr) break;  // uniform per wavefront
+        const float s = quant128(v[j].x, v[j].y, lane, rq + (int64_t)r * kDh);
+        if (lane == 0) rs[r] = s;
+    }
 }
 
 // The per-row quantizations and the vT rows in one launch: the first `rows_blocks` workgroups take the row items
@@ -654,7 +674,7 @@ void attention_rel_quantize(const float *rel_k, int64_t nl, int64_t t, int64_t d
     require(rel_ld >= nl * d && (2 * t - 1) * rel_ld < (1ll << 31), "attention relative rows: bad rel_k row pitch");
     AttnDims D((int)t, (int)d, (int)h);
     D.rel_ld = (int)rel_ld;
-    const dim3 grid((unsigned)((h * D.rp + 3) / 4), (unsigned)nl);
+    const dim3 grid((unsigned)((h * D.rp + 4 * kRelPerWave - 1) / (4 * kRelPerWave)), (unsigned)nl);
     attn_rel_kernel<<<grid, 256, 0, st>>>(rel_k, D, rq, rs);
     hip_check(hipGetLastError(), "attention relative rows kernel launch");
 }
