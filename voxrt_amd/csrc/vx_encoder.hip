@@ -40,11 +40,12 @@ vx_tmat *upload_packed(const uint8_t *qweight, const void *scales, bool scales_f
 void free_tmat(vx_tmat *h);
 void gemm(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y,
           const float *bias, int ep, float alpha, int32_t *gs, int64_t r0, int64_t r1, int64_t t0, int64_t t1,
-          hipStream_t st);
+          hipStream_t st, int64_t cap_rows = 0);
 void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const float *g, const float *b, int8_t *q,
                  float *scales_t, int32_t *gsum_t, hipStream_t stream);
 void gemm_quant(const TMat *w, const int8_t *xq, const float *xs_t, const int32_t *xg_t, int64_t n, float *y_tmp,
-                const float *bias, int ep, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st);
+                const float *bias, int ep, int64_t group, int8_t *q, float *scales_t, int32_t *gsum_t, hipStream_t st,
+                int64_t cap_rows = 0);
 void layer_norm(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y, hipStream_t stream);
 void layer_norm_quantize_ln(const float *x, int64_t n, int64_t d, const float *g, const float *b, float *y,
                             int64_t group, const float *g2, const float *b2, int8_t *q, float *scales_t,
@@ -299,9 +300,12 @@ void ensure_workspace(vx_encoder *e, int64_t t, int64_t nseg, int64_t sub_floats
     }
 }
 
-void gemm_full(const vx_tmat *w, const QBuf &a, int64_t n, float *y, int ep, float alpha, hipStream_t st) {
+// cap: the rows that a and y hold in the workspace (at least n), which lets the streaming kernel run a last
+// partial tile
+void gemm_full(const vx_tmat *w, const QBuf &a, int64_t n, float *y, int ep, float alpha, int64_t cap,
+               hipStream_t st) {
     gemm(&w->m, a.q.as<int8_t>(), a.s.as<float>(), a.g.as<int32_t>(), n, y, nullptr, ep, alpha, nullptr, 0, w->m.out,
-         0, n, st);
+         0, n, st, cap);
 }
 
 // The layer stack of nseg segments of t frames on ws.x[0] (result in ws.x[n_layers % 2]). The token-row work runs
@@ -321,7 +325,7 @@ void run_layers(vx_encoder *e, int64_t t_seg, int64_t nseg, hipStream_t st, Prof
     quantize_ln(e->pos_table.as<float>() + (kMaxFrames - t_seg) * d, np, d, G, nullptr, nullptr, w.posq.q.as<int8_t>(),
                 w.posq.s.as<float>(), w.posq.g.as<int32_t>(), st);
     const int64_t rel_ld = (int64_t)e->layers.size() * d, nl = (int64_t)e->layers.size();
-    gemm_full(e->pos_all, w.posq, np, w.rel_k.as<float>(), VX_EP_STORE, 0.0f, st);
+    gemm_full(e->pos_all, w.posq, np, w.rel_k.as<float>(), VX_EP_STORE, 0.0f, w.np, st);
     // and the attention's quantization of those rows, for all layers in one launch
     const int64_t rrows = attn_rel_rows(t_seg, c.heads), dh = d / c.heads;
     attention_rel_quantize(w.rel_k.as<float>(), nl, t_seg, d, c.heads, rel_ld, w.relq.as<int8_t>(),
@@ -347,14 +351,14 @@ void run_layers(vx_encoder *e, int64_t t_seg, int64_t nseg, hipStream_t st, Prof
             // h = silu(W1 q) quantized for W2 in one call (up to 1024 rows the GEMM quantizes in its epilogue and
             // h never reaches memory; above, hbuf carries it)
             gemm_quant(&L.lin[w1]->m, w.a.q.as<int8_t>(), w.a.s.as<float>(), w.a.g.as<int32_t>(), t, w.hbuf.as<float>(),
-                       nullptr, VX_EP_SILU, G, w.f.q.as<int8_t>(), w.f.s.as<float>(), w.f.g.as<int32_t>(), st);
-            gemm_full(L.lin[w2], w.f, t, x, VX_EP_ADD_SCALED, 0.5f, st);
+                       nullptr, VX_EP_SILU, G, w.f.q.as<int8_t>(), w.f.s.as<float>(), w.f.g.as<int32_t>(), st, w.rows);
+            gemm_full(L.lin[w2], w.f, t, x, VX_EP_ADD_SCALED, 0.5f, w.rows, st);
             mark(kProfFf);
         };
         ffn(0, 0, 1);
         // attention
         lnq(1);
-        gemm_full(L.lin[2], w.a, t, w.qkv.as<float>(), VX_EP_STORE, 0.0f, st);
+        gemm_full(L.lin[2], w.a, t, w.qkv.as<float>(), VX_EP_STORE, 0.0f, w.rows, st);
         mark(kProfAttn);
         if (G == 128) {  // a head's 128 channels are one group: the core writes the o-projection's activations
             attention_core_seg(w.qkv.as<float>(), w.rel_k.as<float>() + li * d, nseg, t_seg, d, c.heads,
@@ -370,11 +374,11 @@ void run_layers(vx_encoder *e, int64_t t_seg, int64_t nseg, hipStream_t st, Prof
             mark(kProfAttnCore);
             quant(w.ctx.as<float>(), d, w.a);
         }
-        gemm_full(L.lin[3], w.a, t, x, VX_EP_ADD_SCALED, 1.0f, st);
+        gemm_full(L.lin[3], w.a, t, x, VX_EP_ADD_SCALED, 1.0f, w.rows, st);
         mark(kProfAttn);
         // convolution module
         lnq(2);
-        gemm_full(L.lin[5], w.a, t, w.g2.as<float>(), VX_EP_STORE, 0.0f, st);
+        gemm_full(L.lin[5], w.a, t, w.g2.as<float>(), VX_EP_STORE, 0.0f, w.rows, st);
         if (G == 128 && d % 256 == 0) {  // the conv rows quantized for pw2 in the same kernel
             glu_dwconv_silu_quant_seg(w.g2.as<float>(), nseg, t_seg, d, c.kconv, L.dw_t.as<float>(),
                                       L.dw_bias.as<float>(), w.a.q.as<int8_t>(), w.a.s.as<float>(), w.a.g.as<int32_t>(),
@@ -384,7 +388,7 @@ void run_layers(vx_encoder *e, int64_t t_seg, int64_t nseg, hipStream_t st, Prof
                                 w.hb.as<float>(), st);
             quant(w.hb.as<float>(), d, w.a);
         }
-        gemm_full(L.lin[6], w.a, t, x, VX_EP_ADD_SCALED, 1.0f, st);
+        gemm_full(L.lin[6], w.a, t, x, VX_EP_ADD_SCALED, 1.0f, w.rows, st);
         mark(kProfConv);
         ffn(3, 7, 8);
         if (li + 1 < e->layers.size()) {  // norm_out, then the next layer's first LayerNorm -> quantize
