@@ -22,9 +22,9 @@
 // Group-sum output (one group, Store): the exact int32 sums S (the fold's operand) are also stored, to the
 // group_sums buffer [1][n][out], beside y.
 //
-// With 16 or more 128-column groups (FFN-down) a second kernel, tgemm_small_ws_kernel, splits each workgroup into
-// producer wavefronts (the MFMA chains) and consumer wavefronts (the fold, one chunk behind), so the fold of one
-// chunk overlaps the loads and MFMAs of the next.
+// With 8, 16 or 32 128-column groups a second kernel, tgemm_small_ws_kernel, splits each workgroup into producer
+// wavefronts (the MFMA chains) and consumer wavefronts (the fold, one chunk behind), so the fold of one chunk
+// overlaps the loads and MFMAs of the next; it is the default for those shapes except the fused quantized output.
 //
 // Quantized output (16 x 128 tiles): instead of y, the epilogue writes the next GEMM's activations. The 16 fold
 // threads of a token hold its 128 outputs of one 128-column group after the epilogue and bias, so the group's
