@@ -145,9 +145,11 @@ __global__ __launch_bounds__(256) void quantize_fast_kernel(const float *__restr
 // slot, where lanes 0-7 run the reference-order statistics. MODE 0 quantizes, MODE 1 writes the LayerNorm row as
 // float32 (y), MODE 2 writes that row to y and then quantizes its LayerNorm with (lg2, lb2): a layer's norm_out
 // followed by the next layer's first LayerNorm->quantize in one pass. Waves of pad tokens [n, np) only write zero
-// scales and code sums, so no pad launch is needed.
-template <int L, int NC, bool LN, int MODE>
-__global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict__ x, int n, int np, int group,
+// scales and code sums, so no pad launch is needed. KEEP (one 1024-column row): the row's LDS column is held in 128
+// registers between the two statistics chains (the shortest chain latency, two wavefronts per SIMD); without it
+// the chains read it in quarters and the kernel fits four wavefronts per SIMD, for launches with many rows.
+template <int L, int NC, bool LN, int MODE, bool KEEP = true>
+__global__ __launch_bounds__(256, KEEP ? 1 : 4) void quant_rows_kernel(const float *__restrict__ x, int n, int np, int group,
                                                         int8_t *__restrict__ q, float *__restrict__ st,
                                                         int32_t *__restrict__ gt, const float *__restrict__ lg,
                                                         const float *__restrict__ lb, float *__restrict__ y,
@@ -217,7 +219,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
         // lane j < 8 keeps the running sum of columns j, j+8, j+16, ... in that order. Each 128-value stretch of
         // its column is read from LDS in one batch before the dependent additions start.
         float s = 0.0f;
-        if constexpr (KL == 128) {
+        if constexpr (KL == 128 && KEEP) {
             // one stretch (1024 columns): all 32 reads issue before the first addition, and the stretch stays in
             // registers for the variance chain
             float4 f[32];
@@ -247,6 +249,48 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
                     qs = __builtin_fmaf(a, a, qs);
                     a = f[k].w - mean;
                     qs = __builtin_fmaf(a, a, qs);
+                }
+            }
+            const float var = hsum8_lanes(qs) / (float)inp;
+            linv = 1.0f / __builtin_sqrtf(var + 1e-5f);
+        } else if constexpr (KL == 128) {
+            // the same chains with the column read in quarters of 32 values (8 reads each)
+            if (lane < 8) {
+                const float *r = T + lane * KLP;
+#pragma unroll
+                for (int k0 = 0; k0 < 32; k0 += 8) {
+                    float4 f[8];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) f[k] = *(const float4 *)(r + 4 * (k0 + k));
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        s += f[k].x;
+                        s += f[k].y;
+                        s += f[k].z;
+                        s += f[k].w;
+                    }
+                }
+            }
+            mean = hsum8_lanes(s) / (float)inp;
+            float qs = 0.0f;
+            if (lane < 8) {
+                const float *r = T + lane * KLP;
+#pragma unroll
+                for (int k0 = 0; k0 < 32; k0 += 8) {
+                    float4 f[8];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) f[k] = *(const float4 *)(r + 4 * (k0 + k));
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        float a = f[k].x - mean;
+                        qs = __builtin_fmaf(a, a, qs);
+                        a = f[k].y - mean;
+                        qs = __builtin_fmaf(a, a, qs);
+                        a = f[k].z - mean;
+                        qs = __builtin_fmaf(a, a, qs);
+                        a = f[k].w - mean;
+                        qs = __builtin_fmaf(a, a, qs);
+                    }
                 }
             }
             const float var = hsum8_lanes(qs) / (float)inp;
@@ -461,6 +505,13 @@ void quantize_ln(const float *x, int64_t n, int64_t inp, int64_t group, const fl
 #define VX_QR(LL, NC)                                                                                                \
     (ln ? quant_rows_kernel<LL, NC, true, 0> : quant_rows_kernel<LL, NC, false, 0>)<<<blk, 256, 0, stream>>>(       \
         x, ni, np, gi, q, scales_t, gsum_t, g, b, nullptr, nullptr, nullptr)
+        // the model's LayerNorm (1024 columns, 128-column groups) over many rows: four wavefronts per SIMD
+        if (ln && L == 8 && nc == 1 && n > 1024) {
+            quant_rows_kernel<8, 1, true, 0, false><<<blk, 256, 0, stream>>>(x, ni, np, gi, q, scales_t, gsum_t, g, b,
+                                                                              nullptr, nullptr, nullptr);
+            hip_check(hipGetLastError(), "quant_rows kernel launch");
+            return;
+        }
 #define VX_QR_NC(LL)                                                                                                 \
     switch (nc) {                                                                                                    \
         case 1: VX_QR(LL, 1); break;                                                                                 \
@@ -560,6 +611,12 @@ void layer_norm_quantize_ln(const float *x, int64_t n, int64_t d, const float *g
         const unsigned blk = (unsigned)((np + 3) / 4);
 #define VX_LQ(LL, NC)                                                                                                \
     quant_rows_kernel<LL, NC, true, 2><<<blk, 256, 0, stream>>>(x, ni, np, gi, q, scales_t, gsum_t, g, b, y, g2, b2)
+        if (group == 128 && d == 1024 && n > 1024) {  // many rows of the model's shape: four wavefronts per SIMD
+            quant_rows_kernel<8, 1, true, 2, false><<<blk, 256, 0, stream>>>(x, ni, np, gi, q, scales_t, gsum_t, g, b,
+                                                                              y, g2, b2);
+            hip_check(hipGetLastError(), "LayerNorm -> quantize kernel launch");
+            return;
+        }
 #define VX_LQ_NC(LL)                                                                                                 \
     switch (d / 1024) {                                                                                              \
         case 1: VX_LQ(LL, 1); break;                                                                                 \
