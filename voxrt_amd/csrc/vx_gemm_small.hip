@@ -764,7 +764,10 @@ bool gemm_small(const GemmArgs &a, hipStream_t st) {
         while (p.d * 2 <= max_ring(1, 8) && steps % (p.d * 2) == 0) p.d *= 2;
         if (grouped && p.d < 2) return false;
         const int n_mt = (int)((a.n + 15) / 16), per_xcd = (p.tiles + 7) / 8;
-        if (grouped && overrides().small_ws.load(std::memory_order_relaxed) == 1) {
+        // up to 128 tokens the producer/consumer kernel (FFN-up at T = 125: 5.51 -> 5.06 us; from 338 tokens the
+        // four-wavefront kernel is faster, 8.27 / 14.3 against 10.1 / 17.9 us at T = 338 / 750)
+        const int wsq = overrides().small_ws.load(std::memory_order_relaxed);
+        if (grouped && (wsq == 1 || (wsq == 0 && a.n <= 128))) {
             const int ft = overrides().small_tile.load(std::memory_order_relaxed);
             if (launch_ws(a, true, ft >> 4, ft & 15, st)) {
                 hip_check(hipGetLastError(), "tgemm_small_ws launch");
