@@ -5,6 +5,8 @@
   workload's per-channel x per-token dequant) and with the model's 128-column groups (f16 scale per (row, group)).
   The calls go through vx_gemm_ep without a group-sum buffer, so the instantiations the bench times run here on
   their real grids. Every output is compared with the oracle's scalar kernel (kernels/mod.rs:166-210), bit for bit.
+- The batched short-clip GEMMs: 64 clips of 2-15 s concatenated to 6987 rows, the FFN, q|k|v and pw1 shapes with
+  one group and with 128-column groups, every output against the same scalar kernel.
 - The 24-layer encoder from log-mel features (Encoder::forward, encoder.rs:816-856): one 60 s segment
   (6000 frames -> T = 750) and 32 segments of 10 s (1000 frames -> T = 125 each) in one batched pass, against the
   oracle's subsampling and 24 conformer layers, bit for bit.
@@ -108,6 +110,48 @@ def test_single_gemm_f32_channel_scales(dev, orc):
     torch.cuda.synchronize()
     q, xs, _ = orc.quantize(x, k)
     _bits_equal(y.cpu().numpy(), orc.gemm(trits, ws, q, xs, k), "338x1024x4096 f32 channel scales")
+    w.free()
+
+
+# ------------------------------------------------------------------------- batched short clips (M = 6987)
+
+@pytest.fixture(scope="module")
+def clip_acts():
+    """The batched short-clip workload's activations: 64 clips of 25 + lcg % 164 frames (2-15 s) concatenated,
+    M = 6987 rows of N(0,1) for K = 1024 and K = 4096, with the bench's seeds."""
+    lens = 25 + synth.Lcg(synth.workload_seed(2, 0)).take(64) % 164
+    m = int(lens.sum())
+    return {k: synth.synth_normal(synth.workload_seed(2, k >> 10), m * k).reshape(m, k) for k in (1024, 4096)}
+
+
+@pytest.mark.parametrize("group", ["K", 128])
+@pytest.mark.parametrize("name,k,n", [("ff_w1", 1024, 4096), ("ff_w2", 4096, 1024), ("qkv", 1024, 3072),
+                                      ("pw1", 1024, 2048)])
+def test_clip_batch_linears(dev, orc, clip_acts, name, k, n, group):
+    """The batched short-clip workload (encoder GEMMs over 64 concatenated clips, Store as the bench times them)
+    at its real row count, 6987 = 54 whole 128-token tiles on the large-token kernels plus 75 rows on the
+    small-token kernels; one group per row and the model's 128-column groups: every output equal to the oracle."""
+    import torch
+
+    import voxrt_amd as vx
+
+    x = clip_acts[k]
+    m = x.shape[0]
+    assert m == 6987
+    G = k if group == "K" else group
+    ng = k // G
+    idx = ("ff_w1", "ff_w2", "qkv", "pw1").index(name)
+    trits = synth.synth_trits(synth.workload_seed(2, 16 + 4 * idx), n, k)
+    s16 = synth.synth_channel_scales_f16(synth.workload_seed(2, 17 + 4 * idx), n, ng) if G == k else \
+        synth.synth_ternary_linear(idx, 1, n, k, G)[1]
+    w = vx.TernaryMatrix.from_packed(synth.pack_rows(trits), s16, n, k, G)
+    xa = vx.QuantAct.quantize(torch.from_numpy(x).to(dev), G)
+    y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+    vx.gemm_ep(w, xa, y, None, vx.Epilogue.Store)
+    torch.cuda.synchronize()
+    q, xs, _ = orc.quantize(x, G)
+    want = orc.gemm(trits, orc.f16_to_f32(s16).reshape(n, ng), q, xs, G, threads=min(16, os.cpu_count() or 1))
+    _bits_equal(y.cpu().numpy(), want, f"clip batch {name} {m}x{k}x{n} G={G}")
     w.free()
 
 

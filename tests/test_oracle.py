@@ -330,6 +330,18 @@ def test_vnni_ternary_equals_scalar_exactly(orc):
             _check_vnni(orc, rng, trits, ws, 128, _acts(rng, n, inp))
 
 
+def test_vnni_ternary_one_group_equals_scalar_exactly(orc):
+    """Ternary weights with one group per row (G = K, the per-channel scales of the GPU's full-size checks):
+    the VNNI restatement equals the scalar kernel bit for bit."""
+    _need_vnni(orc)
+    rng = synth.Lcg(7)
+    for out, inp in [(16, 1024), (37, 4096)]:
+        trits = ((rng.take(out * inp) % 3).astype(np.int8) - 1).reshape(out, inp)
+        ws = (rng.take(out) % 4000 + 100).astype(np.float32) * np.float32(1e-5)
+        for n in [1, 3, 8, 13]:
+            _check_vnni(orc, rng, trits, ws.reshape(out, 1), inp, _acts(rng, n, inp))
+
+
 def test_vnni_int8_equals_scalar_exactly(orc):
     """x86_kernels.rs:154-172 (groups 128, 384, 1024)."""
     _need_vnni(orc)
